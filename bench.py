@@ -1,0 +1,176 @@
+"""Benchmark of the paged-attention hot path on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--config cfg2] [--no-cpu-baseline]
+
+A step is one layer-call of the path at Llama-3-8B decode shapes (BASELINE
+config 2): the slot-mapped KV write of the 64 new tokens (K and V pools) and
+paged GQA decode attention over the block pool, inputs resident in HBM.
+``value`` is the achieved algorithmic HBM bandwidth of the whole step (GB/s);
+``attn_tok_per_s`` the query tokens per second of one layer-call.
+``roofline`` is measured live for the dominant launch (the attention call) with
+HIP events on the stream it runs on; ``cpu_baseline`` times the CPU oracle
+(a restatement of the reference's paged_attn_impl) on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "paged decode attn achieved HBM GB/s (% of peak) + attn tok/s, Llama-3-8B shapes"
+HBM_PEAK_GBS = 8000.0
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_baseline(w, runs: int = 5):
+    """Median wall time of the CPU oracle over the same step (KV write + all
+    (token, head) items), using every host core."""
+    import numpy as np
+    from oracle import oracle
+    sp = w.spec
+    threads = os.cpu_count() or 1
+    kp = w.k_pool.data.cpu().numpy()
+    vp = w.v_pool.data.cpu().numpy()
+    q = w.q.cpu().numpy()
+    kn, vn = w.k_new.cpu().numpy(), w.v_new.cpu().numpy()
+    times = []
+    for i in range(runs + 1):
+        t0 = time.perf_counter()
+        oracle.set_rows(kp, kn, w.slots, sp.kv_type)
+        oracle.set_rows(vp, vn, w.slots, sp.kv_type)
+        oracle.paged_attention(q, kp, vp, sp.kv_type, sp.kv_type, w.block_tables, sp.seq_lens, w.seq_idx, w.pos,
+                               sp.Hkv, sp.D, sp.block_size, sp.scale, softcap=sp.softcap, n_swa=sp.n_swa,
+                               n_threads=threads)
+        dt = time.perf_counter() - t0
+        if i > 0:
+            times.append(dt)
+    med = float(np.median(times))
+    return med, threads
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="cfg2")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU's share: this build runs on a single MI355X "
+              "(multi-GPU sharding is designed, not built); run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+    import iian_amd as pa
+    from iian_amd import synth
+
+    torch.cuda.init()
+    sp = synth.spec(args.config)
+    log(f"building workload {args.config}: S={len(sp.seq_lens)} T={int(sp.n_q.sum())} H={sp.H} Hkv={sp.Hkv} "
+        f"D={sp.D} sum(L)={int(sp.seq_lens.sum())}")
+    w = synth.build(sp, device="cuda")
+    b_step = synth.algorithmic_bytes(w, include_kv_write=True)
+    b_attn = synth.algorithmic_bytes(w, include_kv_write=False)
+    ws = torch.empty(pa.workspace_size(w.T, sp.H, sp.D, w.block_tables.shape[1], sp.block_size),
+                     dtype=torch.uint8, device="cuda")
+    out = torch.empty((w.T, sp.H, sp.D), dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream()
+
+    def kv_write():
+        pa.set_rows(w.k_pool, w.k_new, w.batch.slots)
+        pa.set_rows(w.v_pool, w.v_new, w.batch.slots)
+
+    def attention():
+        pa.build_paged_attn(w.q, w.k_pool, w.v_pool, sp.Hkv, w.params, w.batch, out=out, workspace=ws)
+
+    def step():
+        kv_write()
+        attention()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    log(f"warmup done ({args.warmup} steps)")
+
+    # timed region: exactly K steps, synchronised on both sides
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = wall * 1e3 / args.steps
+    log(f"timed {args.steps} steps: {ms_step * 1e3:.1f} us/step")
+
+    # dominant launch: the attention call alone, HIP events on its stream
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    for a, b in ev:
+        kv_write()
+        a.record(stream)
+        attention()
+        b.record(stream)
+    torch.cuda.synchronize()
+    attn_ms = sum(a.elapsed_time(b) for a, b in ev) / len(ev)
+    attn_gbs = b_attn / (attn_ms * 1e-3) / 1e9
+    log(f"attention: {attn_ms * 1e3:.1f} us/launch, {attn_gbs:.0f} GB/s algorithmic")
+
+    value = b_step / (ms_step * 1e-3) / 1e9
+    res = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"{args.config}: " + {
+                "cfg2": "Llama-3-8B paged decode, H32/Hkv8/D128, 64 seqs, ctx log-uniform [512,8192], "
+                        "16-token f16 blocks in a 65536-block pool, + KV write of 64 tokens",
+            }.get(args.config, args.config),
+            "n_seqs": len(sp.seq_lens), "n_tokens": w.T, "sum_ctx": int(sp.seq_lens.sum()),
+            "algorithmic_bytes_per_step": b_step,
+        },
+        "hbm_frac_of_peak": round(value / HBM_PEAK_GBS, 4),
+        "attn_tok_per_s": round(w.T / (attn_ms * 1e-3), 1),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "iian_pa_attention (pa_decode_f16_kernel + pa_merge_kernel)",
+            "achieved": round(attn_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(attn_gbs / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "algorithmic_bytes_per_launch": b_attn,
+            "avg_launch_us": round(attn_ms * 1e3, 2),
+        },
+    }
+    if not args.no_cpu_baseline:
+        log("timing the CPU oracle on the same step")
+        med, threads = cpu_baseline(w)
+        res["cpu_baseline"] = {
+            "value": round(b_step / med / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"the full {args.config} step (KV write + all {w.T * sp.H} (token, head) items), "
+                      f"median of 5 runs after 1 warm-up, {med * 1e3:.1f} ms/step",
+        }
+    print(json.dumps(res), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,22 @@
+"""iian_amd: MI355X-native paged-attention hot path of the iian inference engine.
+
+The compute lives in libiian_pa.so (hand-written gfx950 HIP kernels behind the
+C ABI of include/iian_pa.h); this package is its host-side mirror of iian's
+operator interface.  Importing it does not require a GPU; calling into the
+kernels does, and fails loudly when the library has not been built.
+"""
+from .paged_attn import (  # noqa: F401
+    GGML_TYPE_F16,
+    GGML_TYPE_F32,
+    GGML_TYPE_Q8_0,
+    KVPool,
+    PagedAttnParams,
+    PagedBatch,
+    build_paged_attn,
+    dequant_q8_0,
+    paged_attn_supported,
+    row_bytes,
+    set_rows,
+    workspace_size,
+)
+from ._lib import PagedAttnError  # noqa: F401

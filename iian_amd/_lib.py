@@ -1,0 +1,72 @@
+"""ctypes binding of libiian_pa.so (the C ABI declared in include/iian_pa.h).
+
+Loading fails loudly: there is no fallback path.  Build the library first with
+``python -m iian_amd.build``.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libiian_pa.so"
+
+OK = 0
+ERR_NULL = -1
+ERR_ARG = -2
+ERR_UNSUPPORTED = -3
+ERR_WORKSPACE = -4
+ERR_HIP = -5
+
+TYPE_F32 = 0
+TYPE_F16 = 1
+TYPE_Q8_0 = 8
+
+# name -> (restype, argtypes); exactly the entry points of include/iian_pa.h
+_P = C.c_void_p
+_I32 = C.c_int32
+_I64 = C.c_int64
+SIGNATURES = {
+    "iian_pa_status_string": (C.c_char_p, [C.c_int]),
+    "iian_pa_supported": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_float]),
+    "iian_pa_kv_write": (C.c_int, [_P, _P, _I64, _I64, _P, _P, _I64, C.c_int, _P]),
+    "iian_pa_workspace_size": (C.c_size_t, [_I32, _I32, _I32, _I32, _I32]),
+    "iian_pa_attention": (C.c_int, [_P, _P, _P, _P, C.c_int, C.c_int, _I32, _P, _I32, _P, _P, _P,
+                                    _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32,
+                                    C.c_float, C.c_float, _I32, _I32, _P, _P, C.c_size_t, _P]),
+    "iian_pa_dequant_q8_0": (C.c_int, [_P, _P, _I64, _P, _I64, _I64, _P]),
+}
+
+_lib = None
+
+
+class PagedAttnError(RuntimeError):
+    """A non-zero status returned by the C ABI."""
+
+    def __init__(self, fn: str, status: int):
+        self.status = status
+        super().__init__(f"{fn} failed: {status} ({status_string(status)})")
+
+
+def load() -> C.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -m iian_amd.build` "
+                           "(there is no CPU fallback for the paged-attention kernels)")
+    lib = C.CDLL(str(LIB_PATH))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def status_string(status: int) -> str:
+    return load().iian_pa_status_string(status).decode()
+
+
+def check(fn: str, status: int) -> None:
+    if status != OK:
+        raise PagedAttnError(fn, status)

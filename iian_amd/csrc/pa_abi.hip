@@ -1,0 +1,173 @@
+// pa_abi.hip - extern "C" boundary of libiian_pa.so (declared in include/iian_pa.h).
+//
+// Host-side argument validation and launch planning; every device launch is
+// asynchronous on the caller's stream.  No exceptions cross the boundary.
+#include "../../include/iian_pa.h"
+#include "pa_common.h"
+#include "pa_launch.h"
+
+#include <cmath>
+
+namespace {
+
+using namespace iian_pa;
+
+// Cells a split-K partition of the decode kernel covers before it splits again.
+constexpr int kSplitCells = 512;
+// Sequences with n_q*gqa up to this many rows run through the decode kernel.
+constexpr int kDecodeRowsMax = 32;
+
+int max_splits_for(int32_t max_blocks, int32_t block_size) {
+    const int64_t cells = (int64_t) max_blocks * block_size + kTile;
+    const int64_t ns = (cells + kSplitCells - 1) / kSplitCells;
+    return (int) (ns < 1 ? 1 : ns);
+}
+
+int log2_exact(int32_t v) {
+    if (v <= 0 || (v & (v - 1))) return -1;
+    int l = 0;
+    while ((1 << l) < v) l++;
+    return l;
+}
+
+int row_bytes(int type, int64_t elems, int64_t &out) {
+    switch (type) {
+        case IIAN_PA_TYPE_F32: out = elems * 4; return 0;
+        case IIAN_PA_TYPE_F16: out = elems * 2; return 0;
+        case IIAN_PA_TYPE_Q8_0:
+            if (elems % 32) return IIAN_PA_ERR_ARG;
+            out = elems / 32 * 34;
+            return 0;
+        default: return IIAN_PA_ERR_UNSUPPORTED;
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *iian_pa_status_string(int status) {
+    switch (status) {
+        case IIAN_PA_OK: return "ok";
+        case IIAN_PA_ERR_NULL: return "a required pointer is NULL";
+        case IIAN_PA_ERR_ARG: return "invalid or inconsistent sizes";
+        case IIAN_PA_ERR_UNSUPPORTED: return "unsupported KV type, head size or ALiBi";
+        case IIAN_PA_ERR_WORKSPACE: return "workspace missing or too small";
+        case IIAN_PA_ERR_HIP: return "HIP runtime error";
+        default: return "unknown status";
+    }
+}
+
+int iian_pa_supported(int type_k, int type_v, int head_dim, int head_dim_v, float max_alibi_bias) {
+    if (max_alibi_bias != 0.0f) return 0;
+    if (type_k != type_v) return 0;
+    if (type_k != IIAN_PA_TYPE_F16) return 0;
+    if (head_dim != head_dim_v) return 0;
+    return head_dim == 64 || head_dim == 128 || head_dim == 256;
+}
+
+int iian_pa_kv_write(void *stream, const float *rows, int64_t n_rows, int64_t row_elems, const int64_t *slots,
+                     void *pool, int64_t n_cells, int type, int32_t *err_flag) {
+    if (n_rows < 0 || row_elems <= 0 || n_cells < 0) return IIAN_PA_ERR_ARG;
+    if (n_rows == 0) return IIAN_PA_OK;
+    if (!rows || !slots || !pool) return IIAN_PA_ERR_NULL;
+    int64_t rb;
+    const int rc = row_bytes(type, row_elems, rb);
+    if (rc) return rc;
+    const hipError_t e = launch_kv_write(rows, n_rows, row_elems, slots, pool, n_cells, type, err_flag,
+                                         (hipStream_t) stream);
+    return e == hipSuccess ? IIAN_PA_OK : IIAN_PA_ERR_HIP;
+}
+
+size_t iian_pa_workspace_size(int32_t n_tokens, int32_t n_head, int32_t head_dim_v, int32_t max_blocks,
+                              int32_t block_size) {
+    if (n_tokens < 0 || n_head <= 0 || head_dim_v <= 0 || max_blocks < 0 || block_size <= 0) return 0;
+    const int ms = max_splits_for(max_blocks, block_size);
+    const size_t rows = (size_t) n_tokens * n_head * ms;
+    const size_t o_bytes = (rows * head_dim_v * sizeof(float) + 255) & ~(size_t) 255;
+    const size_t ml_bytes = (rows * 2 * sizeof(float) + 255) & ~(size_t) 255;
+    return o_bytes + ml_bytes + 256;
+}
+
+int iian_pa_attention(void *stream, const float *q, const void *k_pool, const void *v_pool, int type_k, int type_v,
+                      int32_t num_blocks, const int32_t *block_tables, int32_t max_blocks, const int32_t *seq_lens,
+                      const int32_t *query_start_loc, const int32_t *pos, int32_t n_tokens, int32_t n_seqs,
+                      int32_t max_query_len, int32_t n_head, int32_t n_head_kv, int32_t head_dim, int32_t head_dim_v,
+                      int32_t block_size, float scale, float softcap, int32_t causal, int32_t n_swa, float *out,
+                      void *workspace, size_t workspace_bytes, int32_t *err_flag) {
+    if (n_tokens < 0 || n_seqs < 0 || max_query_len < 0) return IIAN_PA_ERR_ARG;
+    if (n_tokens == 0 || n_seqs == 0) return IIAN_PA_OK;
+    if (!q || !k_pool || !v_pool || !block_tables || !seq_lens || !query_start_loc || !pos || !out)
+        return IIAN_PA_ERR_NULL;
+    if (n_head <= 0 || n_head_kv <= 0 || n_head % n_head_kv) return IIAN_PA_ERR_ARG;
+    if (num_blocks <= 0 || max_blocks <= 0 || max_query_len == 0 || max_query_len > n_tokens) return IIAN_PA_ERR_ARG;
+    if (n_swa < 0 || softcap < 0.0f || !std::isfinite(scale) || !std::isfinite(softcap)) return IIAN_PA_ERR_ARG;
+    const int bs_log2 = log2_exact(block_size);
+    if (bs_log2 < 3) return IIAN_PA_ERR_UNSUPPORTED;   // the 8-cell groups of a tile must not straddle a block
+    if (!iian_pa_supported(type_k, type_v, head_dim, head_dim_v, 0.0f)) return IIAN_PA_ERR_UNSUPPORTED;
+    if (((uintptr_t) q | (uintptr_t) k_pool | (uintptr_t) v_pool | (uintptr_t) out) & 15) return IIAN_PA_ERR_ARG;
+    const size_t need = iian_pa_workspace_size(n_tokens, n_head, head_dim_v, max_blocks, block_size);
+    if (!workspace || workspace_bytes < need) return IIAN_PA_ERR_WORKSPACE;
+
+    AttnParams p = {};
+    p.q = q;
+    p.k_pool = (const char *) k_pool;
+    p.v_pool = (const char *) v_pool;
+    p.bt = block_tables;
+    p.seq_lens = seq_lens;
+    p.qsl = query_start_loc;
+    p.pos = pos;
+    p.out = out;
+    p.err = err_flag;
+    int64_t kr, vr;
+    if (row_bytes(type_k, (int64_t) n_head_kv * head_dim, kr) || row_bytes(type_v, (int64_t) n_head_kv * head_dim_v, vr))
+        return IIAN_PA_ERR_ARG;
+    p.k_row = kr;
+    p.v_row = vr;
+    p.max_blocks = max_blocks;
+    p.num_blocks = num_blocks;
+    p.T = n_tokens;
+    p.S = n_seqs;
+    p.H = n_head;
+    p.Hkv = n_head_kv;
+    p.gqa = n_head / n_head_kv;
+    p.bs_log2 = bs_log2;
+    p.softcap = softcap;
+    p.softcap_inv = softcap > 0.0f ? 1.0f / softcap : 0.0f;
+    // exp2-domain softmax: fold log2(e) into q unless the softcap has to see the raw score first
+    p.qscale = softcap > 0.0f ? scale : scale * kLog2e;
+    p.causal = causal ? 1 : 0;
+    p.n_swa = n_swa;
+    p.max_splits = max_splits_for(max_blocks, block_size);
+    p.split_cells = kSplitCells;
+    const size_t rows = (size_t) n_tokens * n_head * p.max_splits;
+    const size_t o_bytes = (rows * head_dim_v * sizeof(float) + 255) & ~(size_t) 255;
+    char *ws = (char *) (((uintptr_t) workspace + 255) & ~(uintptr_t) 255);
+    p.part_o = (float *) ws;
+    p.part_ml = (float *) (ws + o_bytes);
+
+    // Row budget of the decode kernel: one 16-row MFMA tile, or two when that
+    // covers every sequence of the call (spec-verify); larger sequences go to
+    // the prefill kernel.
+    const int max_rows = max_query_len * p.gqa;
+    p.decode_rows = (max_rows > 16 && max_rows <= kDecodeRowsMax) ? kDecodeRowsMax : 16;
+    hipStream_t st = (hipStream_t) stream;
+    hipError_t e = launch_decode(p, head_dim, type_k, st);
+    if (e != hipSuccess) return IIAN_PA_ERR_HIP;
+    if (max_rows > p.decode_rows) {
+        e = launch_prefill(p, head_dim, type_k, max_rows, st);
+        if (e != hipSuccess) return IIAN_PA_ERR_HIP;
+    }
+    return IIAN_PA_OK;
+}
+
+int iian_pa_dequant_q8_0(void *stream, const void *pool, int64_t n_cells, const int64_t *rows_idx, int64_t n_rows,
+                         int64_t row_elems, float *out) {
+    if (n_rows < 0 || row_elems <= 0 || row_elems % 32 || n_cells < 0) return IIAN_PA_ERR_ARG;
+    if (n_rows == 0) return IIAN_PA_OK;
+    if (!pool || !rows_idx || !out) return IIAN_PA_ERR_NULL;
+    const hipError_t e = launch_dequant_q8_0(pool, n_cells, rows_idx, n_rows, row_elems, out, (hipStream_t) stream);
+    return e == hipSuccess ? IIAN_PA_OK : IIAN_PA_ERR_HIP;
+}
+
+}  // extern "C"

@@ -1,0 +1,127 @@
+// pa_common.h - shared device-side types and helpers of the gfx950 paged-attention kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace iian_pa {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kTile = 32;   // cells per KV tile (two 16-row MFMA halves)
+
+// Everything the attention kernels read, by value (kernel argument segment).
+struct AttnParams {
+    const float *q;             // [T][H][D]
+    const char *k_pool;         // cell rows of Hkv*D elements
+    const char *v_pool;
+    const int32_t *bt;          // [S][max_blocks]
+    const int32_t *seq_lens;    // [S]
+    const int32_t *qsl;         // [S+1]
+    const int32_t *pos;         // [T]
+    float *out;                 // [T][H][Dv]
+    float *part_o;              // [T][H][max_splits][Dv]   split-K partial numerators
+    float *part_ml;             // [T][H][max_splits][2]    (running max in log2 units, sum)
+    int32_t *err;               // nullable error word
+    int64_t k_row;              // bytes per K pool row
+    int64_t v_row;
+    int32_t max_blocks;
+    int32_t num_blocks;
+    int32_t T, S, H, Hkv, gqa;
+    int32_t bs_log2;
+    float qscale;               // folded into q before the f16 conversion
+    float softcap;              // 0 = off
+    float softcap_inv;
+    int32_t causal;
+    int32_t n_swa;
+    int32_t max_splits;
+    int32_t split_cells;
+    int32_t decode_rows;        // sequences with n_q*gqa <= decode_rows use the decode kernel
+};
+
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, __shfl_xor(v, 16));
+    v = fmaxf(v, __shfl_xor(v, 32));
+    return v;
+}
+
+// Physical block id of logical block b of sequence s, clamped into the table
+// row and the pool (a seq_len beyond the table's capacity or a stale block id
+// is flagged, never dereferenced).
+__device__ __forceinline__ int32_t phys_block(const AttnParams &p, int s, int b) {
+    if (b >= p.max_blocks) {
+        if (p.err) atomicOr(p.err, 2);
+        b = p.max_blocks - 1;
+    }
+    int32_t id = p.bt[(int64_t) s * p.max_blocks + b];
+    if ((uint32_t) id >= (uint32_t) p.num_blocks) {
+        if (p.err) atomicOr(p.err, 2);
+        id = 0;
+    }
+    return id;
+}
+
+// Cell window of sequence s that any of its query tokens can attend, and its
+// split-K partition.  Identical in the attention and merge kernels.
+struct SeqWindow {
+    int L, q0, nq;
+    int pmin, pmax;
+    int c_lo, c_hi;     // [c_lo, c_hi): c_lo a multiple of kTile
+    int chunk, nsplit;
+};
+
+__device__ __forceinline__ void split_plan(int range, int split_cells, int max_splits, int &chunk, int &nsplit) {
+    if (range <= 0) { chunk = kTile; nsplit = 1; return; }
+    chunk = split_cells;
+    nsplit = (range + chunk - 1) / chunk;
+    if (nsplit > max_splits) {
+        chunk = (((range + max_splits - 1) / max_splits) + kTile - 1) & ~(kTile - 1);
+        nsplit = (range + chunk - 1) / chunk;
+    }
+}
+
+// pmin/pmax over the sequence's query positions (wave-cooperative; all lanes get the result).
+__device__ __forceinline__ void seq_window(const AttnParams &p, int s, SeqWindow &w) {
+    const int lane = threadIdx.x & 63;
+    w.L = p.seq_lens[s];
+    w.q0 = min(max(p.qsl[s], 0), p.T);
+    w.nq = min(max(p.qsl[s + 1], w.q0), p.T) - w.q0;
+    int mn = INT32_MAX, mx = INT32_MIN;
+    for (int i = lane; i < w.nq; i += 64) {
+        const int ps = p.pos[w.q0 + i];
+        mn = min(mn, ps);
+        mx = max(mx, ps);
+    }
+    for (int o = 32; o >= 1; o >>= 1) {
+        mn = min(mn, __shfl_xor(mn, o));
+        mx = max(mx, __shfl_xor(mx, o));
+    }
+    w.pmin = mn;
+    w.pmax = mx;
+    int hi = w.L;
+    if (p.causal) hi = min(hi, w.pmax + 1);
+    int lo = 0;
+    if (p.n_swa > 0) lo = max(0, w.pmin - p.n_swa + 1);
+    lo &= ~(kTile - 1);
+    if (hi < lo) hi = lo;
+    w.c_lo = lo;
+    w.c_hi = hi;
+    split_plan(hi - lo, p.split_cells, p.max_splits, w.chunk, w.nsplit);
+}
+
+__device__ __forceinline__ bool cell_masked(int c, int L, int prow, int causal, int n_swa) {
+    return c >= L || (causal && c > prow) || (n_swa > 0 && prow - c >= n_swa);
+}
+
+__device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
+    const _Float16 ha = (_Float16) a, hb = (_Float16) b;
+    return (uint32_t) __builtin_bit_cast(uint16_t, ha) | ((uint32_t) __builtin_bit_cast(uint16_t, hb) << 16);
+}
+
+}  // namespace iian_pa

@@ -1,0 +1,18 @@
+// pa_launch.h - internal launchers shared between the kernel files and the C ABI layer.
+#pragma once
+
+#include "pa_common.h"
+
+namespace iian_pa {
+
+// Decode / spec-verify kernel (sequences with n_q*gqa <= p.decode_rows) plus the split-K merge.
+hipError_t launch_decode(const AttnParams &p, int head_dim, int kv_type, hipStream_t stream);
+// MFMA prefill kernel (sequences with n_q*gqa > p.decode_rows); grid covers max_query_len*gqa rows.
+hipError_t launch_prefill(const AttnParams &p, int head_dim, int kv_type, int max_rows, hipStream_t stream);
+
+hipError_t launch_kv_write(const float *rows, int64_t n_rows, int64_t row_elems, const int64_t *slots, void *pool,
+                           int64_t n_cells, int type, int32_t *err, hipStream_t stream);
+hipError_t launch_dequant_q8_0(const void *pool, int64_t n_cells, const int64_t *rows_idx, int64_t n_rows,
+                               int64_t row_elems, float *out, hipStream_t stream);
+
+}  // namespace iian_pa

@@ -1,0 +1,292 @@
+// pa_prefill.hip - chunked-prefill causal paged attention for gfx950 (MFMA f16, LDS-staged KV).
+//
+// One workgroup of NW waves per (row block, kv head, sequence); rows are
+// r = j*gqa + g (query token j, head g of the GQA group), NRT 16-row MFMA tiles
+// per wave.  The workgroup streams the sequence's cells in 32-cell tiles
+// through the block table into LDS (register-staged double buffer) and every
+// wave reuses each tile for all its rows:
+//
+//   S^T = K * Q^T       v_mfma_f32_16x16x32_f16, K rows read from LDS with
+//                       ds_read_b128 as the A operand, Q^T from registers
+//   online softmax      exp2 domain; causal / sliding-window masks only on
+//                       tiles that straddle a boundary; waves skip tiles that
+//                       are fully masked for all their rows
+//   O += P * V          P from registers (A operand); V^T B operands come
+//                       straight from the row-major LDS tile through the
+//                       gfx950 transpose read ds_read_b64_tr_b16
+//
+// Workgroups of one (kv head, sequence) share their K/V and are placed on one
+// XCD (its L2) by remapping the linear workgroup id.
+// Semantics: paged_attn_impl (src/iian/paged_attn.cpp:90-146).
+#include "pa_common.h"
+#include "pa_launch.h"
+
+namespace iian_pa {
+
+template <int D>
+struct PrefillShape {
+    static constexpr int KS = D / 32;                 // QK^T k-steps
+    static constexpr int NPV = D / 16;                // PV MFMAs (16 output dims each)
+    static constexpr int STRIDE = D * 2 + 16;         // padded LDS row (bytes)
+    static constexpr int TILE_BYTES = kTile * STRIDE;
+    static constexpr int CHUNKS = kTile * (D / 8);    // 16-byte chunks per tile per tensor
+};
+
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+__device__ __forceinline__ f16x8 lds_tr_b16x8(const char *p0, const char *p1) {
+    const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *) (uintptr_t) p0);
+    const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *) (uintptr_t) p1);
+    typedef short s16x8 __attribute__((ext_vector_type(8)));
+    const s16x8 c = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+    return __builtin_bit_cast(f16x8, c);
+}
+
+template <int D, int NRT, int NW>
+__global__ __launch_bounds__(NW * 64) void pa_prefill_f16_kernel(AttnParams p, int n_rb) {
+    using SH = PrefillShape<D>;
+    constexpr int KS = SH::KS, NPV = SH::NPV, STRIDE = SH::STRIDE;
+    constexpr int CPT = SH::CHUNKS / (NW * 64);   // 16-byte chunks per thread per tensor
+    static_assert(CPT * NW * 64 == SH::CHUNKS, "tile chunks must divide evenly");
+    constexpr int ROWS = NW * NRT * 16;
+    __shared__ __attribute__((aligned(16))) char lds[2][2][SH::TILE_BYTES];
+
+    // XCD-aware remap: consecutive logical ids (same kv head / sequence) share an XCD.
+    const int total = n_rb * p.Hkv * p.S;
+    const int nwg = gridDim.x;
+    const int bid = blockIdx.x;
+    const int logical = (bid & 7) * (nwg >> 3) + (bid >> 3);
+    if (logical >= total) return;
+    const int rb = logical % n_rb;
+    const int hk = (logical / n_rb) % p.Hkv;
+    const int s = logical / (n_rb * p.Hkv);
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, n = lane & 15;
+    const int L = p.seq_lens[s];
+    const int q0 = min(max(p.qsl[s], 0), p.T);
+    const int nq = min(max(p.qsl[s + 1], q0), p.T) - q0;
+    const int M = nq * p.gqa;
+    if (M <= p.decode_rows) return;
+    const int R0 = rb * ROWS;
+    if (R0 >= M) return;
+
+    // positions of this workgroup's and this wave's rows
+    const int Rw = R0 + wave * NRT * 16;
+    int wg_min = INT32_MAX, wg_max = INT32_MIN, w_min = INT32_MAX, w_max = INT32_MIN;
+    {
+        const int j0 = R0 / p.gqa, j1 = (min(M, R0 + ROWS) - 1) / p.gqa;
+        for (int j = j0 + lane; j <= j1; j += 64) {
+            const int ps = p.pos[q0 + j];
+            wg_min = min(wg_min, ps);
+            wg_max = max(wg_max, ps);
+        }
+        if (Rw < M) {
+            const int k0 = Rw / p.gqa, k1 = (min(M, Rw + NRT * 16) - 1) / p.gqa;
+            for (int j = k0 + lane; j <= k1; j += 64) {
+                const int ps = p.pos[q0 + j];
+                w_min = min(w_min, ps);
+                w_max = max(w_max, ps);
+            }
+        }
+        for (int o = 32; o >= 1; o >>= 1) {
+            wg_min = min(wg_min, __shfl_xor(wg_min, o));
+            wg_max = max(wg_max, __shfl_xor(wg_max, o));
+            w_min = min(w_min, __shfl_xor(w_min, o));
+            w_max = max(w_max, __shfl_xor(w_max, o));
+        }
+    }
+    const bool wave_live = Rw < M;
+    int c_hi = L;
+    if (p.causal) c_hi = min(c_hi, wg_max + 1);
+    int c_lo = 0;
+    if (p.n_swa > 0) c_lo = max(0, wg_min - p.n_swa + 1);
+    c_lo &= ~(kTile - 1);
+
+    // Q^T B operands, row positions, running state
+    f16x8 qv[NRT][KS];
+    int prow[NRT];
+    float m_run[NRT], l_run[NRT];
+    f32x4 o[NRT][NPV];
+#pragma unroll
+    for (int rt = 0; rt < NRT; rt++) {
+        const int r = Rw + rt * 16 + n;
+        prow[rt] = wave_live ? w_max : 0;
+        if (r < M) {
+            const int t = q0 + r / p.gqa, h = hk * p.gqa + r % p.gqa;
+            prow[rt] = p.pos[t];
+            const float *qp = p.q + ((int64_t) t * p.H + h) * D + 8 * g;
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) {
+                const float4 a = *(const float4 *) (qp + 32 * ks);
+                const float4 b = *(const float4 *) (qp + 32 * ks + 4);
+                const u32x4 u = {pack_f16x2(a.x * p.qscale, a.y * p.qscale), pack_f16x2(a.z * p.qscale, a.w * p.qscale),
+                                 pack_f16x2(b.x * p.qscale, b.y * p.qscale), pack_f16x2(b.z * p.qscale, b.w * p.qscale)};
+                qv[rt][ks] = __builtin_bit_cast(f16x8, u);
+            }
+        } else {
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) qv[rt][ks] = __builtin_bit_cast(f16x8, u32x4{0u, 0u, 0u, 0u});
+        }
+        m_run[rt] = -INFINITY;
+        l_run[rt] = 0.f;
+#pragma unroll
+        for (int m = 0; m < NPV; m++) o[rt][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    const int bs_mask = (1 << p.bs_log2) - 1;
+    const int64_t head_off = (int64_t) hk * D * 2;
+    u32x4 kst[CPT], vst[CPT];
+    auto load_global = [&](int tile) {
+#pragma unroll
+        for (int j = 0; j < CPT; j++) {
+            const int q = tid + j * NW * 64;
+            const int cell = q / (D / 8), col = q % (D / 8);
+            const int c = min(tile + cell, L - 1);
+            const int64_t row = ((int64_t) phys_block(p, s, c >> p.bs_log2) << p.bs_log2) | (c & bs_mask);
+            kst[j] = *(const u32x4 *) (p.k_pool + row * p.k_row + head_off + col * 16);
+            vst[j] = *(const u32x4 *) (p.v_pool + row * p.v_row + head_off + col * 16);
+        }
+    };
+    auto store_lds = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < CPT; j++) {
+            const int q = tid + j * NW * 64;
+            const int cell = q / (D / 8), col = q % (D / 8);
+            *(u32x4 *) (&lds[buf][0][cell * STRIDE + col * 16]) = kst[j];
+            *(u32x4 *) (&lds[buf][1][cell * STRIDE + col * 16]) = vst[j];
+        }
+    };
+
+    auto compute = [&](int tile, int buf) {
+        if (!wave_live) return;
+        if (p.causal && tile > w_max) return;                              // every cell after every row
+        if (p.n_swa > 0 && tile + kTile - 1 <= w_min - p.n_swa) return;   // every cell out of every window
+        const bool full = tile + kTile <= L && (!p.causal || tile + kTile - 1 <= w_min) &&
+                          (p.n_swa <= 0 || w_max - tile < p.n_swa);
+        const char *Kl = lds[buf][0];
+        const char *Vl = lds[buf][1];
+        f16x8 ka[2][KS];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int cr = 8 * (n >> 2) + 4 * h + (n & 3);
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) ka[h][ks] = *(const f16x8 *) (Kl + cr * STRIDE + (32 * ks + 8 * g) * 2);
+        }
+        f16x8 pa[NRT];
+#pragma unroll
+        for (int rt = 0; rt < NRT; rt++) {
+            float sv[8];
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < KS; ks++) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[h][ks], qv[rt][ks], acc, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; i++) sv[4 * h + i] = acc[i];
+            }
+            if (p.softcap > 0.f) {
+#pragma unroll
+                for (int e = 0; e < 8; e++) sv[e] = p.softcap * tanhf(sv[e] * p.softcap_inv) * kLog2e;
+            }
+            if (!full) {
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    if (cell_masked(tile + 8 * g + e, L, prow[rt], p.causal, p.n_swa)) sv[e] = -INFINITY;
+            }
+            float mt = sv[0];
+#pragma unroll
+            for (int e = 1; e < 8; e++) mt = fmaxf(mt, sv[e]);
+            mt = wave_max(mt);
+            const float mnew = fmaxf(m_run[rt], mt);
+            float alpha = 1.f;
+            float pv[8];
+            if (mnew == -INFINITY) {
+#pragma unroll
+                for (int e = 0; e < 8; e++) pv[e] = 0.f;
+            } else {
+                alpha = __builtin_amdgcn_exp2f(m_run[rt] - mnew);
+#pragma unroll
+                for (int e = 0; e < 8; e++) pv[e] = __builtin_amdgcn_exp2f(sv[e] - mnew);
+            }
+            m_run[rt] = mnew;
+            float ps = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; e++) ps += pv[e];
+            l_run[rt] = l_run[rt] * alpha + ps;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float a = __shfl(alpha, 4 * g + i);
+#pragma unroll
+                for (int m = 0; m < NPV; m++) o[rt][m][i] *= a;
+            }
+            u32x4 pk;
+#pragma unroll
+            for (int wi = 0; wi < 4; wi++) pk[wi] = pack_f16x2(pv[2 * wi], pv[2 * wi + 1]);
+            pa[rt] = __builtin_bit_cast(f16x8, pk);
+        }
+        const char *vrow = Vl + (8 * g + (n >> 2)) * STRIDE + 8 * (n & 3);
+#pragma unroll
+        for (int m = 0; m < NPV; m++) {
+            const f16x8 vb = lds_tr_b16x8(vrow + 32 * m, vrow + 4 * STRIDE + 32 * m);
+#pragma unroll
+            for (int rt = 0; rt < NRT; rt++) o[rt][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[rt], vb, o[rt][m], 0, 0, 0);
+        }
+    };
+
+    if (c_lo < c_hi) {
+        int buf = 0;
+        load_global(c_lo);
+        store_lds(0);
+        __syncthreads();
+        for (int tile = c_lo; tile < c_hi; tile += kTile) {
+            const bool has_next = tile + kTile < c_hi;
+            if (has_next) load_global(tile + kTile);
+            compute(tile, buf);
+            if (has_next) store_lds(buf ^ 1);
+            __syncthreads();
+            buf ^= 1;
+        }
+    }
+
+    if (!wave_live) return;
+#pragma unroll
+    for (int rt = 0; rt < NRT; rt++) {
+        float l = l_run[rt];
+        l += __shfl_xor(l, 16);
+        l += __shfl_xor(l, 32);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int r = Rw + rt * 16 + 4 * g + i;
+            const float lr = __shfl(l, 4 * g + i);
+            if (r < M) {
+                const int t = q0 + r / p.gqa, h = hk * p.gqa + r % p.gqa;
+                const float inv = lr > 0.f ? 1.f / lr : 0.f;
+                float *op = p.out + ((int64_t) t * p.H + h) * D + n;
+#pragma unroll
+                for (int m = 0; m < NPV; m++) op[16 * m] = o[rt][m][i] * inv;
+            }
+        }
+    }
+}
+
+template <int D, int NRT, int NW>
+static hipError_t launch_prefill_t(const AttnParams &p, int max_rows, hipStream_t stream) {
+    constexpr int ROWS = NW * NRT * 16;
+    const int n_rb = (max_rows + ROWS - 1) / ROWS;
+    const int total = n_rb * p.Hkv * p.S;
+    const int nwg = (total + 7) & ~7;
+    hipLaunchKernelGGL((pa_prefill_f16_kernel<D, NRT, NW>), dim3(nwg), dim3(NW * 64), 0, stream, p, n_rb);
+    return hipGetLastError();
+}
+
+hipError_t launch_prefill(const AttnParams &p, int head_dim, int kv_type, int max_rows, hipStream_t stream) {
+    if (kv_type != 1) return hipErrorInvalidValue;
+    switch (head_dim) {
+        case 64: return launch_prefill_t<64, 2, 4>(p, max_rows, stream);
+        case 128: return launch_prefill_t<128, 2, 4>(p, max_rows, stream);
+        case 256: return launch_prefill_t<256, 2, 4>(p, max_rows, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace iian_pa

@@ -1,0 +1,237 @@
+"""Host-side mirror of iian's paged-attention operator over the gfx950 C ABI.
+
+Names and argument meaning follow the reference (CocoRoF/iian):
+
+* ``PagedAttnParams``        src/iian/paged_attn.h:16-22 (the UBatch pointer
+                             becomes the explicit ``PagedBatch`` argument)
+* ``paged_attn_supported``   src/iian/paged_attn.cpp:15-18
+* ``set_rows``               ggml_set_rows as build_attn uses it for the KV
+                             write, src/iian/graph.cpp:314-322
+* ``build_paged_attn``       src/iian/paged_attn.h:29-30 / paged_attn.cpp:159-169:
+                             q [T][H][D] f32 -> out [T][H][Dv] f32
+* ``PagedBatch.from_ubatch`` the UBatch of include/iian/graph.h:22-38 as the
+                             engine fills it (src/iian/engine.cpp:491-535),
+                             compressed losslessly to block tables
+
+Where the reference aborts on a violated precondition (GGML_ASSERT in
+paged_attn.cpp:161-162 and ggml-cpu/ops.cpp:5263) this layer raises
+``PagedAttnError`` / ``ValueError`` instead.  All device work goes through
+libiian_pa.so; torch is used only for device memory and streams.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+from typing import Optional, Sequence
+
+import numpy as np
+import torch
+
+from . import _lib
+
+GGML_TYPE_F32 = _lib.TYPE_F32
+GGML_TYPE_F16 = _lib.TYPE_F16
+GGML_TYPE_Q8_0 = _lib.TYPE_Q8_0
+QK8_0 = 32
+Q8_0_BLOCK_BYTES = 34
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def row_bytes(type_: int, n: int) -> int:
+    """ggml_row_size for the pool types."""
+    if type_ == GGML_TYPE_F32:
+        return 4 * n
+    if type_ == GGML_TYPE_F16:
+        return 2 * n
+    if type_ == GGML_TYPE_Q8_0:
+        if n % QK8_0:
+            raise ValueError("Q8_0 rows need a multiple of 32 elements")
+        return n // QK8_0 * Q8_0_BLOCK_BYTES
+    raise ValueError(f"unsupported ggml type {type_}")
+
+
+@dataclass
+class PagedAttnParams:
+    """src/iian/paged_attn.h:16-22."""
+    scale: float = 1.0
+    softcap: float = 0.0      # 0 = off
+    causal: bool = True
+    n_swa: int = 0            # 0 = full attention for this layer
+
+
+class KVPool:
+    """One layer's K or V cell pool: ``n_cells`` rows of ``n_embd`` elements of
+    ``type_`` (src/iian/kv_cache.cpp:156-169), zero-initialised like the
+    reference's ggml_backend_buffer_clear (kv_cache.cpp:173)."""
+
+    def __init__(self, n_cells: int, n_embd: int, type_: int, device="cuda"):
+        self.n_cells = n_cells
+        self.n_embd = n_embd
+        self.type = type_
+        self.row_bytes = row_bytes(type_, n_embd)
+        self.data = torch.zeros((n_cells, self.row_bytes), dtype=torch.uint8, device=device)
+
+    @classmethod
+    def wrap(cls, data: torch.Tensor, n_embd: int, type_: int) -> "KVPool":
+        """Use an existing [n_cells, row_bytes] byte tensor as the pool."""
+        self = cls.__new__(cls)
+        self.n_cells = data.shape[0]
+        self.n_embd = n_embd
+        self.type = type_
+        self.row_bytes = row_bytes(type_, n_embd)
+        if data.dtype != torch.uint8 or data.dim() != 2 or data.shape[1] != self.row_bytes or not data.is_contiguous():
+            raise ValueError("pool tensor must be contiguous uint8 [n_cells, row_bytes]")
+        self.data = data
+        return self
+
+    def view_f16(self) -> torch.Tensor:
+        if self.type != GGML_TYPE_F16:
+            raise ValueError("not an f16 pool")
+        return self.data.view(torch.float16)
+
+
+@dataclass
+class PagedBatch:
+    """Device-side description of a micro-batch (the UBatch of
+    include/iian/graph.h:22-38 with each sequence's cell list given as its
+    block table; cell_pos[i] == i always holds, engine.cpp:505)."""
+    block_tables: torch.Tensor      # int32 [S, max_blocks]
+    seq_lens: torch.Tensor          # int32 [S]
+    query_start_loc: torch.Tensor   # int32 [S+1]
+    pos: torch.Tensor               # int32 [T]
+    slots: torch.Tensor             # int64 [T]
+    max_query_len: int
+    block_size: int = 16
+
+    @property
+    def n_tokens(self) -> int:
+        return int(self.pos.shape[0])
+
+    @property
+    def n_seqs(self) -> int:
+        return int(self.seq_lens.shape[0])
+
+    @classmethod
+    def from_ubatch(cls, pos: Sequence[int], seq_idx: Sequence[int], slots: Sequence[int],
+                    seq_cells: Sequence[Sequence[int]], block_size: int = 16,
+                    seq_cell_pos: Optional[Sequence[Sequence[int]]] = None, device="cuda") -> "PagedBatch":
+        """Compress a reference UBatch (per-token pos/seq_idx/slots, per-sequence
+        absolute cells) into block tables.  Raises ValueError when the cells are
+        not block-structured (cell i must be table[i // bs] * bs + i % bs,
+        kv_cache.h:135-137), when cell_pos[i] != i, or when a sequence's tokens
+        are not contiguous in the batch (engine.cpp:508-513 builds them so)."""
+        seq_idx = np.asarray(seq_idx, dtype=np.int64)
+        S = len(seq_cells)
+        T = len(pos)
+        if len(seq_idx) != T or len(slots) != T:
+            raise ValueError("pos, seq_idx and slots must have one entry per token")
+        if T and (seq_idx.min() < 0 or seq_idx.max() >= S):
+            raise ValueError("seq_idx out of range")
+        if T and np.any(np.diff(seq_idx) < 0):
+            raise ValueError("tokens of a sequence must be contiguous and sequences in order")
+        counts = np.bincount(seq_idx, minlength=S) if T else np.zeros(S, dtype=np.int64)
+        qsl = np.zeros(S + 1, dtype=np.int32)
+        qsl[1:] = np.cumsum(counts)
+        lens = np.array([len(c) for c in seq_cells], dtype=np.int32)
+        max_blocks = max(1, int(((lens.max() if S else 0) + block_size - 1) // block_size))
+        bt = np.zeros((S, max_blocks), dtype=np.int32)
+        for s, cells in enumerate(seq_cells):
+            cells = np.asarray(cells, dtype=np.int64)
+            if seq_cell_pos is not None and not np.array_equal(np.asarray(seq_cell_pos[s]), np.arange(len(cells))):
+                raise ValueError("cell_pos[i] must equal i")
+            nb = (len(cells) + block_size - 1) // block_size
+            for b in range(nb):
+                seg = cells[b * block_size:(b + 1) * block_size]
+                blk = seg[0] // block_size
+                if seg[0] % block_size or not np.array_equal(seg, blk * block_size + np.arange(len(seg))):
+                    raise ValueError(f"sequence {s}: cells are not block-structured at block {b}")
+                bt[s, b] = blk
+        t = lambda a, dt: torch.as_tensor(np.asarray(a), dtype=dt, device=device)
+        return cls(block_tables=t(bt, torch.int32), seq_lens=t(lens, torch.int32),
+                   query_start_loc=t(qsl, torch.int32), pos=t(pos, torch.int32), slots=t(slots, torch.int64),
+                   max_query_len=int(counts.max()) if S else 0, block_size=block_size)
+
+
+def paged_attn_supported(type_k: int, type_v: int, max_alibi_bias: float, head_dim: int = 128,
+                         head_dim_v: Optional[int] = None) -> bool:
+    """src/iian/paged_attn.cpp:15-18, as supported by the gfx950 kernels."""
+    lib = _lib.load()
+    return bool(lib.iian_pa_supported(type_k, type_v, head_dim, head_dim if head_dim_v is None else head_dim_v,
+                                      float(max_alibi_bias)))
+
+
+def set_rows(pool: KVPool, rows: torch.Tensor, slots: torch.Tensor, err_flag: Optional[torch.Tensor] = None) -> KVPool:
+    """ggml_set_rows(pool, rows, slots) (src/iian/graph.cpp:319-320): row
+    slots[t] of the pool <- convert(rows[t]).  rows: f32 [T, n_embd]."""
+    if rows.dtype != torch.float32 or rows.dim() != 2 or rows.shape[1] != pool.n_embd:
+        raise ValueError("rows must be f32 [n_tokens, n_embd]")
+    if slots.dtype != torch.int64 or slots.shape != (rows.shape[0],):
+        raise ValueError("slots must be int64 [n_tokens]")
+    rows = rows.contiguous()
+    lib = _lib.load()
+    st = lib.iian_pa_kv_write(_stream(), rows.data_ptr(), rows.shape[0], rows.shape[1], slots.data_ptr(),
+                              pool.data.data_ptr(), pool.n_cells, pool.type, _ptr(err_flag))
+    _lib.check("iian_pa_kv_write", st)
+    return pool
+
+
+def workspace_size(n_tokens: int, n_head: int, head_dim_v: int, max_blocks: int, block_size: int) -> int:
+    return int(_lib.load().iian_pa_workspace_size(n_tokens, n_head, head_dim_v, max_blocks, block_size))
+
+
+def build_paged_attn(q: torch.Tensor, k_cache: KVPool, v_cache: KVPool, n_head_kv: int,
+                     params: PagedAttnParams, batch: PagedBatch, out: Optional[torch.Tensor] = None,
+                     workspace: Optional[torch.Tensor] = None,
+                     err_flag: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Paged attention of q [T, H, D] over the pools (paged_attn.cpp:90-169);
+    returns f32 [T, H, Dv]."""
+    if q.dtype != torch.float32 or q.dim() != 3:
+        raise ValueError("q must be f32 [n_tokens, n_head, head_dim]")   # paged_attn.cpp:161
+    if not q.is_contiguous():
+        raise ValueError("q head vectors must be contiguous")            # paged_attn.cpp:162
+    T, H, D = q.shape
+    if k_cache.n_embd % n_head_kv or v_cache.n_embd % n_head_kv:
+        raise ValueError("pool rows must hold n_head_kv heads")
+    if k_cache.n_embd // n_head_kv != D:
+        raise ValueError("k head size differs from q head size")
+    Dv = v_cache.n_embd // n_head_kv
+    if T != batch.n_tokens:
+        raise ValueError("q and batch disagree on n_tokens")
+    if k_cache.n_cells != v_cache.n_cells or k_cache.n_cells % batch.block_size:
+        raise ValueError("pools must hold the same whole number of blocks")
+    num_blocks = k_cache.n_cells // batch.block_size
+    if out is None:
+        out = torch.empty((T, H, Dv), dtype=torch.float32, device=q.device)
+    max_blocks = int(batch.block_tables.shape[1])
+    need = workspace_size(T, H, Dv, max_blocks, batch.block_size)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    lib = _lib.load()
+    st = lib.iian_pa_attention(_stream(), q.data_ptr(), k_cache.data.data_ptr(), v_cache.data.data_ptr(),
+                               k_cache.type, v_cache.type, num_blocks, batch.block_tables.data_ptr(), max_blocks,
+                               batch.seq_lens.data_ptr(), batch.query_start_loc.data_ptr(), batch.pos.data_ptr(),
+                               T, batch.n_seqs, batch.max_query_len, H, n_head_kv, D, Dv, batch.block_size,
+                               float(params.scale), float(params.softcap), int(bool(params.causal)),
+                               int(params.n_swa), out.data_ptr(), workspace.data_ptr(), workspace.numel(),
+                               _ptr(err_flag))
+    _lib.check("iian_pa_attention", st)
+    return out
+
+
+def dequant_q8_0(pool: KVPool, rows_idx: torch.Tensor) -> torch.Tensor:
+    """f32 values of the given Q8_0 pool rows (ggml-quants.c:553-567)."""
+    if pool.type != GGML_TYPE_Q8_0:
+        raise ValueError("not a Q8_0 pool")
+    rows_idx = rows_idx.to(torch.int64).contiguous()
+    out = torch.empty((rows_idx.shape[0], pool.n_embd), dtype=torch.float32, device=pool.data.device)
+    st = _lib.load().iian_pa_dequant_q8_0(_stream(), pool.data.data_ptr(), pool.n_cells, rows_idx.data_ptr(),
+                                          rows_idx.shape[0], pool.n_embd, out.data_ptr())
+    _lib.check("iian_pa_dequant_q8_0", st)
+    return out

@@ -1,0 +1,124 @@
+/*
+ * iian_pa.h - C ABI of the MI355X paged-attention library (libiian_pa.so).
+ *
+ * Drop-in for the two operations iian's attention layer performs on the paged
+ * KV cache (CocoRoF/iian, paths relative to its source tree):
+ *   1. the slot-mapped KV write   ggml_set_rows(cache, rows, slots)
+ *                                 (src/iian/graph.cpp:314-322, executed by
+ *                                 ggml-cpu/ops.cpp:5221-5289)
+ *   2. paged attention            build_paged_attn / paged_attn_op
+ *                                 (src/iian/paged_attn.h:16-30,
+ *                                 src/iian/paged_attn.cpp:90-169)
+ *
+ * Conventions
+ *   - Every entry point is extern "C", returns an int status (IIAN_PA_OK = 0,
+ *     negative on error) and never throws.
+ *   - Every pointer argument except `stream` is a device pointer (HBM).  All
+ *     launches are asynchronous on `stream` (a hipStream_t; NULL = the null
+ *     stream).  The caller owns all buffers; the library keeps nothing between
+ *     calls except a cached device-property query.
+ *   - Type codes are ggml's enum ggml_type values: F32 = 0, F16 = 1, Q8_0 = 8.
+ *   - Pool layout is the reference's (src/iian/kv_cache.cpp:156-169): one row
+ *     per cell holding all KV heads, K row = Hkv*D elements, V row = Hkv*Dv
+ *     elements, rows contiguous; Q8_0 rows are (Hkv*D/32) blocks of 34 bytes
+ *     (ggml-common.h:251-256).  Cell of token i of sequence s is
+ *     block_tables[s*max_blocks + i/block_size]*block_size + i%block_size
+ *     (include/iian/kv_cache.h:135-137).
+ */
+#ifndef IIAN_PA_H
+#define IIAN_PA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    IIAN_PA_OK = 0,
+    IIAN_PA_ERR_NULL = -1,         /* a required pointer is NULL */
+    IIAN_PA_ERR_ARG = -2,          /* inconsistent sizes / shapes */
+    IIAN_PA_ERR_UNSUPPORTED = -3,  /* dtype / head size / ALiBi not supported */
+    IIAN_PA_ERR_WORKSPACE = -4,    /* workspace missing or too small */
+    IIAN_PA_ERR_HIP = -5           /* a HIP runtime call failed */
+};
+
+enum { IIAN_PA_TYPE_F32 = 0, IIAN_PA_TYPE_F16 = 1, IIAN_PA_TYPE_Q8_0 = 8 };
+
+/* Human-readable text of a status code (static storage). */
+const char *iian_pa_status_string(int status);
+
+/* Replaces paged_attn_supported (src/iian/paged_attn.cpp:15-18), widened to
+ * Q8_0 and to the head sizes the kernels are built for.  Returns 1 when
+ * iian_pa_attention accepts this combination, else 0.  K and V must have the
+ * same type (F16 or Q8_0), head_dim == head_dim_v in {64, 128, 256}, and no
+ * ALiBi (max_alibi_bias == 0). */
+int iian_pa_supported(int type_k, int type_v, int head_dim, int head_dim_v, float max_alibi_bias);
+
+/* Replaces ggml_set_rows(cache, rows, slots) on the K or V pool
+ * (src/iian/graph.cpp:319-320; CPU semantics ggml-cpu/ops.cpp:5221-5289):
+ *   pool row slots[t] <- convert(rows[t]),  t in [0, n_rows)
+ * rows: f32 [n_rows][row_elems]; slots: int64 [n_rows]; pool: n_cells rows of
+ * `type` (F16: IEEE round-to-nearest-even; Q8_0: ggml's x86 quantiser,
+ * ggml-cpu/arch/x86/quants.c:302-398).  Slots must be distinct within a call
+ * (ggml.h:1693).  A slot outside [0, n_cells) is not written and sets bit 0 of
+ * *err_flag when err_flag is non-NULL (the reference aborts,
+ * ggml-cpu/ops.cpp:5263). */
+int iian_pa_kv_write(void *stream, const float *rows, int64_t n_rows, int64_t row_elems,
+                     const int64_t *slots, void *pool, int64_t n_cells, int type,
+                     int32_t *err_flag);
+
+/* Bytes of device workspace iian_pa_attention needs for these sizes (split-K
+ * partial results).  Returns 0 on invalid arguments. */
+size_t iian_pa_workspace_size(int32_t n_tokens, int32_t n_head, int32_t head_dim_v,
+                              int32_t max_blocks, int32_t block_size);
+
+/* Replaces build_paged_attn + paged_attn_op (src/iian/paged_attn.h:29-30,
+ * src/iian/paged_attn.cpp:90-169).  For every query token t and head h:
+ *   out[t][h][:] = sum_c softmax_c(s_c) * V[cell_c][hk][:],
+ *   s_c = scale * <q[t][h], K[cell_c][hk]>  (then softcap*tanh(s/softcap)
+ *   when softcap > 0), hk = h / (H/Hkv),
+ * over the cells c in [0, seq_lens[s]) of the token's sequence s that are not
+ * masked: masked when (causal && c > pos[t]) || (n_swa > 0 && pos[t]-c >= n_swa)
+ * (paged_attn.cpp:124).  A token with every cell masked gets a zero row
+ * (paged_attn.cpp:132).
+ *   q               f32 [T][H][D] (contiguous head vectors, paged_attn.cpp:161-162)
+ *   k_pool, v_pool  the cell pools of one layer, num_blocks*block_size rows
+ *   block_tables    int32 [S][max_blocks] physical block ids
+ *   seq_lens        int32 [S] cells of each sequence, this step's included
+ *                   (UBatch::SeqInfo::cells.size(), include/iian/graph.h:33-36)
+ *   query_start_loc int32 [S+1] tokens of sequence s are
+ *                   [query_start_loc[s], query_start_loc[s+1]) (the
+ *                   reference's per-token UBatch::seq_idx, whose tokens are
+ *                   contiguous per sequence, engine.cpp:508-513)
+ *   pos             int32 [T] UBatch::pos
+ *   max_query_len   host int: max tokens of one sequence in this call
+ *   out             f32 [T][H][Dv]
+ *   workspace       device scratch of at least iian_pa_workspace_size(...) bytes
+ * Block ids outside [0, num_blocks) are clamped (never dereferenced out of the
+ * pool) and set bit 1 of *err_flag when err_flag is non-NULL. */
+int iian_pa_attention(void *stream, const float *q, const void *k_pool, const void *v_pool,
+                      int type_k, int type_v, int32_t num_blocks,
+                      const int32_t *block_tables, int32_t max_blocks,
+                      const int32_t *seq_lens, const int32_t *query_start_loc,
+                      const int32_t *pos, int32_t n_tokens, int32_t n_seqs,
+                      int32_t max_query_len, int32_t n_head, int32_t n_head_kv,
+                      int32_t head_dim, int32_t head_dim_v, int32_t block_size,
+                      float scale, float softcap, int32_t causal, int32_t n_swa,
+                      float *out, void *workspace, size_t workspace_bytes,
+                      int32_t *err_flag);
+
+/* Dequantises n_rows Q8_0 rows of row_elems values each (pool rows
+ * rows_idx[i]) to f32, bit-exactly as ggml's dequantize_row_q8_0
+ * (ggml-quants.c:553-567).  Exposes the values the attention kernels feed into
+ * their arithmetic so that they can be checked bit for bit.  Rows outside
+ * [0, n_cells) produce zeros. */
+int iian_pa_dequant_q8_0(void *stream, const void *pool, int64_t n_cells, const int64_t *rows_idx,
+                         int64_t n_rows, int64_t row_elems, float *out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,340 @@
+/*
+ * pa_oracle.c - CPU restatement of iian's paged-attention path (the oracle).
+ *
+ * TEST INFRASTRUCTURE ONLY: the checker the HIP kernels are compared against.
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+ * load it; the product library never does.
+ *
+ * Parity status of each function (how it is pinned; tests/test_oracle.py):
+ *   pao_f32_to_f16 / pao_f16_to_f32    numpy float16 casts (IEEE RNE), all
+ *                                       65536 halves and 2^20 random floats
+ *   pao_quantize_row_q8_0 (+ _ref)      bit-exact against ggml's own
+ *                                       quantize_row_q8_0 / _ref compiled
+ *                                       from the reference tree (oracle/_ref),
+ *                                       plus a tie case separating RNE from
+ *                                       roundf
+ *   pao_dequantize_row_q8_0             ggml's dequantize_row_q8_0 (oracle/_ref)
+ *                                       and the closed form q*fp32(d)
+ *   pao_set_rows                        closed form: placement by slot, all
+ *                                       other rows untouched
+ *   pao_paged_attention                 float64 brute-force softmax(qK^T)V
+ *                                       with explicit masks, and invariants
+ *                                       (block permutation, prefix sharing,
+ *                                       thread count, single cell, SWA >= ctx)
+ * The reference's paged_attn.cpp itself cannot be built here (it links
+ * ggml.c, which needs the CMake-generated ggml-version.h), so the exact fp32
+ * bits of paged_attn_impl are restated, not compared.
+ */
+#include "pa_oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+#if defined(__F16C__)
+#include <immintrin.h>
+#endif
+
+/* ------------------------------------------------------------------ fp16 */
+
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* IEEE binary32 -> binary16, round to nearest even, written from the format
+ * definitions.  Restates the conversion of ggml-cpu.c:3480-3499 (F16C,
+ * _MM_FROUND_TO_NEAREST_INT); NaNs keep their top payload bits and are
+ * quietened as F16C does. */
+uint16_t pao_f32_to_f16(float f) {
+    const uint32_t x = f2u(f);
+    const uint16_t sign = (uint16_t) ((x >> 16) & 0x8000u);
+    const uint32_t ax = x & 0x7fffffffu;
+    if (ax >= 0x7f800000u) {                       /* inf / nan */
+        if (ax == 0x7f800000u) return sign | 0x7c00u;
+        return sign | 0x7e00u | (uint16_t) ((ax >> 13) & 0x3ffu);
+    }
+    const int e = (int) (ax >> 23) - 127;
+    if (e >= 16) return sign | 0x7c00u;             /* overflow -> inf */
+    if (e >= -14) {                                 /* normal half */
+        const uint32_t mant = ax & 0x7fffffu;
+        uint32_t h = ((uint32_t) (e + 15) << 10) | (mant >> 13);
+        const uint32_t rem = mant & 0x1fffu;
+        if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;  /* may carry into inf */
+        return sign | (uint16_t) h;
+    }
+    if (e < -25) return sign;                       /* below half of the smallest subnormal */
+    /* subnormal half: value = m24 * 2^(e-23), unit 2^-24 */
+    const uint32_t m24 = (ax & 0x7fffffu) | 0x800000u;
+    const int sh = -(e + 1);                        /* 14 .. 24 */
+    uint32_t h = m24 >> sh;
+    const uint32_t rem = m24 & ((1u << sh) - 1u);
+    const uint32_t half = 1u << (sh - 1);
+    if (rem > half || (rem == half && (h & 1u))) h++;
+    return sign | (uint16_t) h;
+}
+
+/* binary16 -> binary32, exact (ggml-impl.h:384-405 computes the same value). */
+float pao_f16_to_f32(uint16_t hv) {
+    const uint32_t sign = ((uint32_t) hv & 0x8000u) << 16;
+    const uint32_t ex = (hv >> 10) & 0x1fu;
+    const uint32_t m = hv & 0x3ffu;
+    if (ex == 0x1fu) return u2f(sign | 0x7f800000u | (m << 13));
+    if (ex == 0) {
+        if (m == 0) return u2f(sign);
+        /* subnormal: m * 2^-24, exact in binary32 */
+        const float v = (float) m * 0x1p-24f;
+        return sign ? -v : v;
+    }
+    return u2f(sign | ((ex + 112u) << 23) | (m << 13));
+}
+
+void pao_f32_to_f16_row(const float *x, uint16_t *y, int64_t n) {
+    for (int64_t i = 0; i < n; i++) y[i] = pao_f32_to_f16(x[i]);
+}
+
+void pao_f16_to_f32_row(const uint16_t *x, float *y, int64_t n) {
+    int64_t i = 0;
+#if defined(__F16C__) && defined(__AVX__)
+    for (; i + 8 <= n; i += 8)
+        _mm256_storeu_ps(y + i, _mm256_cvtph_ps(_mm_loadu_si128((const __m128i *) (x + i))));
+#endif
+    for (; i < n; i++) y[i] = pao_f16_to_f32(x[i]);
+}
+
+/* ------------------------------------------------------------------ Q8_0 */
+
+typedef struct { uint16_t d; int8_t qs[PAO_QK8_0]; } q8_0_block;   /* ggml-common.h:251-256 */
+_Static_assert(sizeof(q8_0_block) == PAO_Q8_0_BLOCK_BYTES, "block_q8_0 is 34 bytes");
+
+static inline int8_t sat_i8(int32_t v) {   /* packs_epi32 then packs_epi16 saturate */
+    if (v > 127) return 127;
+    if (v < -128) return -128;
+    return (int8_t) v;
+}
+
+/* ggml-cpu/arch/x86/quants.c:302-398 (the AVX2 branch the reference engine
+ * runs on the MI355X host): per 32 values amax = max|x|, d = amax/127.f,
+ * stored as f16(d); id = 127.f/amax (0 when amax == 0); q = RNE(x*id). */
+void pao_quantize_row_q8_0(const float *x, void *vy, int64_t k) {
+    q8_0_block *y = (q8_0_block *) vy;
+    const int64_t nb = k / PAO_QK8_0;
+    for (int64_t b = 0; b < nb; b++) {
+        const float *xb = x + b * PAO_QK8_0;
+        float amax = 0.0f;
+        for (int j = 0; j < PAO_QK8_0; j++) { const float a = fabsf(xb[j]); amax = a > amax ? a : amax; }
+        const float d = amax / 127.f;
+        y[b].d = pao_f32_to_f16(d);
+        const float id = amax != 0.0f ? 127.f / amax : 0.0f;
+        for (int j = 0; j < PAO_QK8_0; j++) y[b].qs[j] = sat_i8((int32_t) nearbyintf(xb[j] * id));
+    }
+}
+
+/* ggml-quants.c:276-299: id = 1/d and roundf (ties away from zero). */
+void pao_quantize_row_q8_0_ref(const float *x, void *vy, int64_t k) {
+    q8_0_block *y = (q8_0_block *) vy;
+    const int64_t nb = k / PAO_QK8_0;
+    for (int64_t b = 0; b < nb; b++) {
+        const float *xb = x + b * PAO_QK8_0;
+        float amax = 0.0f;
+        for (int j = 0; j < PAO_QK8_0; j++) amax = fmaxf(amax, fabsf(xb[j]));
+        const float d = amax / 127;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        y[b].d = pao_f32_to_f16(d);
+        for (int j = 0; j < PAO_QK8_0; j++) y[b].qs[j] = (int8_t) roundf(xb[j] * id);
+    }
+}
+
+/* ggml-quants.c:553-567 */
+void pao_dequantize_row_q8_0(const void *vx, float *y, int64_t k) {
+    const q8_0_block *x = (const q8_0_block *) vx;
+    const int64_t nb = k / PAO_QK8_0;
+    for (int64_t b = 0; b < nb; b++) {
+        const float d = pao_f16_to_f32(x[b].d);
+        for (int j = 0; j < PAO_QK8_0; j++) y[b * PAO_QK8_0 + j] = (float) x[b].qs[j] * d;
+    }
+}
+
+int64_t pao_row_bytes(int type, int64_t n) {
+    switch (type) {
+        case PAO_F32: return n * 4;
+        case PAO_F16: return n * 2;
+        case PAO_Q8_0: return (n / PAO_QK8_0) * PAO_Q8_0_BLOCK_BYTES;
+        default: return -1;
+    }
+}
+
+/* ------------------------------------------------------------- KV write */
+
+/* ggml-cpu/ops.cpp:5221-5289 for an f32 source: for each row i, the index
+ * slots[i] must satisfy 0 <= idx < ne1 (GGML_ASSERT :5263) and the row is
+ * written with the destination type's from_float (ggml-cpu.c:222-227,
+ * 272-273). */
+int pao_set_rows(const float *rows, int64_t n_rows, int64_t row_elems,
+                 const int64_t *slots, void *pool, int64_t n_cells, int type) {
+    const int64_t rb = pao_row_bytes(type, row_elems);
+    if (rb < 0 || (type == PAO_Q8_0 && row_elems % PAO_QK8_0)) return -2;
+    for (int64_t i = 0; i < n_rows; i++)
+        if (slots[i] < 0 || slots[i] >= n_cells) return -1;
+    for (int64_t i = 0; i < n_rows; i++) {
+        const float *src = rows + i * row_elems;
+        char *dst = (char *) pool + slots[i] * rb;
+        if (type == PAO_F32) memcpy(dst, src, (size_t) rb);
+        else if (type == PAO_F16) pao_f32_to_f16_row(src, (uint16_t *) dst, row_elems);
+        else pao_quantize_row_q8_0(src, dst, row_elems);
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------ attention */
+
+/* Kern<T>::dot of paged_attn.cpp:25-71: two 8-lane FMA accumulators over
+ * 16-wide strides, one more 8-wide step, lane-wise a0+a1, then the eight
+ * lanes summed left to right; scalar tail after that. */
+static inline float dot_f32(const float *q, const float *k, int D) {
+    float a0[8] = {0}, a1[8] = {0};
+    int i = 0;
+    for (; i + 16 <= D; i += 16)
+        for (int j = 0; j < 8; j++) {
+            a0[j] = fmaf(q[i + j], k[i + j], a0[j]);
+            a1[j] = fmaf(q[i + 8 + j], k[i + 8 + j], a1[j]);
+        }
+    for (; i + 8 <= D; i += 8)
+        for (int j = 0; j < 8; j++) a0[j] = fmaf(q[i + j], k[i + j], a0[j]);
+    for (int j = 0; j < 8; j++) a0[j] += a1[j];
+    float s = a0[0] + a0[1] + a0[2] + a0[3] + a0[4] + a0[5] + a0[6] + a0[7];
+    for (; i < D; i++) s = fmaf(q[i], k[i], s);
+    return s;
+}
+
+/* Kern<T>::axpy of paged_attn.cpp:43-53,77-86: acc += p*v, 8-wide FMA. */
+static inline void axpy_f32(float *acc, float p, const float *v, int D) {
+    for (int i = 0; i < D; i++) acc[i] = fmaf(p, v[i], acc[i]);
+}
+
+typedef struct {
+    const float *q;
+    const char *k_pool, *v_pool;
+    int k_type, v_type;
+    const int32_t *bt;
+    int32_t max_blocks;
+    const int32_t *seq_lens, *seq_idx, *pos;
+    int32_t T, S, H, Hkv, D, Dv, bs;
+    float scale, softcap;
+    int32_t causal, n_swa;
+    float *out;
+    const int64_t *items;
+    int64_t n_items;
+    int64_t k_row, v_row;      /* bytes per cell row */
+    int32_t max_len;
+    int64_t i0, i1;            /* this worker's item range */
+} pa_job;
+
+/* Widen one head slice of one cell row to f32 (F16 as in F16C cvtph,
+ * Q8_0 via dequantize_row_q8_0, F32 copied). */
+static inline const float *head_row(const char *pool, int type, int64_t row_bytes, int64_t cell,
+                                    int hk, int d, float *buf) {
+    const char *row = pool + cell * row_bytes;
+    if (type == PAO_F32) return (const float *) row + (int64_t) hk * d;
+    if (type == PAO_F16) { pao_f16_to_f32_row((const uint16_t *) row + (int64_t) hk * d, buf, d); return buf; }
+    pao_dequantize_row_q8_0(row + (int64_t) hk * (d / PAO_QK8_0) * PAO_Q8_0_BLOCK_BYTES, buf, d);
+    return buf;
+}
+
+/* paged_attn_impl<TK,TV> (paged_attn.cpp:90-146) over items [i0, i1). */
+static void *pa_worker(void *arg) {
+    pa_job *J = (pa_job *) arg;
+    float *scores = (float *) malloc(sizeof(float) * (size_t) (J->max_len > 0 ? J->max_len : 1));
+    float *acc = (float *) malloc(sizeof(float) * (size_t) J->Dv);
+    float *kbuf = (float *) malloc(sizeof(float) * (size_t) J->D);
+    float *vbuf = (float *) malloc(sizeof(float) * (size_t) J->Dv);
+    const int gqa = J->H / J->Hkv;
+    for (int64_t ii = J->i0; ii < J->i1; ii++) {
+        const int64_t it = J->items ? J->items[ii] : ii;
+        const int64_t t = it / J->H, h = it % J->H, hk = h / gqa;
+        const float *qv = J->q + (t * J->H + h) * J->D;
+        const int32_t s = J->seq_idx[t];
+        const int32_t p1 = J->pos[t];
+        const int32_t n_cells = J->seq_lens[s];
+        const int32_t *bt = J->bt + (int64_t) s * J->max_blocks;
+        /* pass 1: scores and max over the cells this query may attend (:121-130) */
+        float mx = -INFINITY;
+        for (int32_t c = 0; c < n_cells; c++) {
+            const int32_t p0 = c;   /* cell_pos[c] == c (engine.cpp:505) */
+            if ((J->causal && p0 > p1) || (J->n_swa > 0 && p1 - p0 >= J->n_swa)) { scores[c] = -INFINITY; continue; }
+            const int64_t cell = (int64_t) bt[c / J->bs] * J->bs + c % J->bs;   /* kv_cache.h:135-137 */
+            const float *kp = head_row(J->k_pool, J->k_type, J->k_row, cell, (int) hk, J->D, kbuf);
+            float sc = dot_f32(qv, kp, J->D) * J->scale;
+            if (J->softcap > 0.0f) sc = J->softcap * tanhf(sc / J->softcap);
+            scores[c] = sc;
+            mx = mx < sc ? sc : mx;
+        }
+        float *o = J->out + (t * J->H + h) * J->Dv;
+        if (mx == -INFINITY) { for (int i = 0; i < J->Dv; i++) o[i] = 0.0f; continue; }   /* :132 */
+        /* pass 2: softmax weights and the weighted V sum (:134-144) */
+        for (int i = 0; i < J->Dv; i++) acc[i] = 0.0f;
+        float sum = 0.0f;
+        for (int32_t c = 0; c < n_cells; c++) {
+            if (scores[c] == -INFINITY) continue;
+            const float p = expf(scores[c] - mx);
+            sum += p;
+            const int64_t cell = (int64_t) bt[c / J->bs] * J->bs + c % J->bs;
+            const float *vp = head_row(J->v_pool, J->v_type, J->v_row, cell, (int) hk, J->Dv, vbuf);
+            axpy_f32(acc, p, vp, J->Dv);
+        }
+        const float inv = 1.0f / sum;
+        for (int i = 0; i < J->Dv; i++) o[i] = acc[i] * inv;
+    }
+    free(scores); free(acc); free(kbuf); free(vbuf);
+    return NULL;
+}
+
+static int type_ok(int t) { return t == PAO_F32 || t == PAO_F16 || t == PAO_Q8_0; }
+
+int pao_paged_attention(const float *q, const void *k_pool, const void *v_pool,
+                        int k_type, int v_type,
+                        const int32_t *block_tables, int32_t max_blocks,
+                        const int32_t *seq_lens, const int32_t *seq_idx,
+                        const int32_t *pos, int32_t T, int32_t S, int32_t H,
+                        int32_t Hkv, int32_t D, int32_t Dv, int32_t block_size,
+                        float scale, float softcap, int32_t causal, int32_t n_swa,
+                        float *out, int32_t n_threads,
+                        const int64_t *items, int64_t n_items) {
+    if (!q || !k_pool || !v_pool || !block_tables || !seq_lens || !seq_idx || !pos || !out) return -1;
+    if (T < 0 || S <= 0 || H <= 0 || Hkv <= 0 || H % Hkv || D <= 0 || Dv <= 0 || block_size <= 0) return -2;
+    if (!type_ok(k_type) || !type_ok(v_type)) return -3;
+    if ((k_type == PAO_Q8_0 && D % PAO_QK8_0) || (v_type == PAO_Q8_0 && Dv % PAO_QK8_0)) return -3;
+    int32_t max_len = 0;
+    for (int32_t s = 0; s < S; s++) {
+        if (seq_lens[s] < 0 || seq_lens[s] > max_blocks * block_size) return -4;
+        if (seq_lens[s] > max_len) max_len = seq_lens[s];
+    }
+    for (int32_t t = 0; t < T; t++)
+        if (seq_idx[t] < 0 || seq_idx[t] >= S) return -5;
+    pa_job base;
+    memset(&base, 0, sizeof base);
+    base.q = q; base.k_pool = (const char *) k_pool; base.v_pool = (const char *) v_pool;
+    base.k_type = k_type; base.v_type = v_type; base.bt = block_tables; base.max_blocks = max_blocks;
+    base.seq_lens = seq_lens; base.seq_idx = seq_idx; base.pos = pos;
+    base.T = T; base.S = S; base.H = H; base.Hkv = Hkv; base.D = D; base.Dv = Dv; base.bs = block_size;
+    base.scale = scale; base.softcap = softcap; base.causal = causal; base.n_swa = n_swa;
+    base.out = out; base.items = items;
+    base.k_row = pao_row_bytes(k_type, (int64_t) Hkv * D);
+    base.v_row = pao_row_bytes(v_type, (int64_t) Hkv * Dv);
+    base.max_len = max_len;
+    const int64_t n = items ? n_items : (int64_t) T * H;
+    int nth = n_threads > 0 ? n_threads : 1;
+    if (nth > 256) nth = 256;
+    /* contiguous chunks per thread, as paged_attn.cpp:103-106 */
+    const int64_t per = (n + nth - 1) / nth;
+    pa_job jobs[256];
+    pthread_t tid[256];
+    for (int i = 0; i < nth; i++) {
+        jobs[i] = base;
+        jobs[i].i0 = (int64_t) i * per < n ? (int64_t) i * per : n;
+        jobs[i].i1 = jobs[i].i0 + per < n ? jobs[i].i0 + per : n;
+    }
+    if (nth == 1) { pa_worker(&jobs[0]); return 0; }
+    for (int i = 0; i < nth; i++) pthread_create(&tid[i], NULL, pa_worker, &jobs[i]);
+    for (int i = 0; i < nth; i++) pthread_join(tid[i], NULL);
+    return 0;
+}

@@ -1,0 +1,148 @@
+"""C-ABI checks that need no GPU: the library loads, exports every entry point
+of include/iian_pa.h, and rejects invalid arguments on the host before any
+device work (the reference aborts on these, paged_attn.cpp:161-162 and
+ggml-cpu/ops.cpp:5263; the ABI returns status codes instead)."""
+import ctypes as C
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from iian_amd import _lib
+    return _lib.load()
+
+
+def header_symbols():
+    text = (ROOT / "include" / "iian_pa.h").read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[\w\s\*]+?\b(iian_pa_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol(lib):
+    from iian_amd import _lib
+    syms = header_symbols()
+    assert len(syms) >= 6
+    for s in syms:
+        assert hasattr(lib, s), s
+    assert set(syms) == set(_lib.SIGNATURES)
+
+
+def test_status_strings(lib):
+    from iian_amd import _lib
+    for code in (_lib.OK, _lib.ERR_NULL, _lib.ERR_ARG, _lib.ERR_UNSUPPORTED, _lib.ERR_WORKSPACE, _lib.ERR_HIP):
+        assert _lib.status_string(code) not in ("", "unknown status")
+    assert _lib.status_string(12345) == "unknown status"
+
+
+def test_supported_matrix(lib):
+    from iian_amd import paged_attn_supported as sup
+    F32, F16, Q8 = 0, 1, 8
+    assert sup(F16, F16, 0.0, 128)
+    assert sup(F16, F16, 0.0, 64) and sup(F16, F16, 0.0, 256)
+    assert not sup(F16, F16, 8.0, 128)          # ALiBi (paged_attn.cpp:17)
+    assert not sup(F16, F32, 0.0, 128)          # mixed K/V types
+    assert not sup(F16, F16, 0.0, 96)           # head size without a kernel
+    assert not sup(F16, F16, 0.0, 128, 64)      # Dv != D
+
+
+def test_workspace_size(lib):
+    from iian_amd import workspace_size
+    a = workspace_size(64, 32, 128, 512, 16)
+    b = workspace_size(64, 32, 128, 1024, 16)
+    assert 0 < a < b
+    assert workspace_size(-1, 32, 128, 512, 16) == 0
+    assert workspace_size(0, 32, 128, 512, 16) > 0
+
+
+def call_attention(lib, **over):
+    """iian_pa_attention with a valid-looking argument set (fake but aligned
+    device addresses: every case here must be rejected before any launch)."""
+    a = dict(stream=None, q=0x1000, k=0x2000, v=0x3000, tk=1, tv=1, num_blocks=64, bt=0x4000, max_blocks=4,
+             seq_lens=0x5000, qsl=0x6000, pos=0x7000, T=4, S=2, maxq=2, H=8, Hkv=2, D=128, Dv=128, bs=16,
+             scale=0.1, softcap=0.0, causal=1, n_swa=0, out=0x8000, ws=0x9000, ws_bytes=1 << 30, err=None)
+    a.update(over)
+    return lib.iian_pa_attention(a["stream"], a["q"], a["k"], a["v"], a["tk"], a["tv"], a["num_blocks"], a["bt"],
+                                 a["max_blocks"], a["seq_lens"], a["qsl"], a["pos"], a["T"], a["S"], a["maxq"],
+                                 a["H"], a["Hkv"], a["D"], a["Dv"], a["bs"], a["scale"], a["softcap"], a["causal"],
+                                 a["n_swa"], a["out"], a["ws"], a["ws_bytes"], a["err"])
+
+
+@pytest.mark.parametrize("over,code", [
+    ({"q": None}, -1), ({"k": None}, -1), ({"bt": None}, -1), ({"out": None}, -1), ({"pos": None}, -1),
+    ({"H": 6, "Hkv": 4}, -2), ({"Hkv": 0}, -2), ({"T": -1}, -2), ({"maxq": 5}, -2), ({"num_blocks": 0}, -2),
+    ({"n_swa": -1}, -2), ({"softcap": -1.0}, -2), ({"scale": float("nan")}, -2), ({"q": 0x1004}, -2),
+    ({"tk": 8, "tv": 8}, -3), ({"tk": 0, "tv": 0}, -3), ({"tk": 1, "tv": 0}, -3), ({"D": 96, "Dv": 96}, -3),
+    ({"bs": 12}, -3), ({"bs": 4}, -3),
+    ({"ws": None}, -4), ({"ws_bytes": 16}, -4),
+])
+def test_attention_rejects_invalid_arguments(lib, over, code):
+    assert call_attention(lib, **over) == code
+
+
+def test_attention_empty_batch_is_ok(lib):
+    assert call_attention(lib, T=0) == 0
+    assert call_attention(lib, S=0) == 0
+
+
+def test_kv_write_rejects_invalid_arguments(lib):
+    # every call here must return before any launch (the pointers are fake)
+    f = lib.iian_pa_kv_write
+    assert f(None, None, 4, 128, 0x2000, 0x3000, 64, 1, None) == -1
+    assert f(None, 0x1000, 4, 128, None, 0x3000, 64, 1, None) == -1
+    assert f(None, 0x1000, -1, 128, 0x2000, 0x3000, 64, 1, None) == -2
+    assert f(None, 0x1000, 4, 100, 0x2000, 0x3000, 64, 8, None) == -2      # Q8_0 needs 32-multiples
+    assert f(None, 0x1000, 4, 128, 0x2000, 0x3000, 64, 2, None) == -3      # Q4_0 not a KV write type here
+    assert f(None, 0x1000, 0, 128, 0x2000, 0x3000, 64, 1, None) == 0       # nothing to do
+
+
+def test_dequant_rejects_invalid_arguments(lib):
+    f = lib.iian_pa_dequant_q8_0
+    assert f(None, None, 64, 0x2000, 4, 128, 0x3000) == -1
+    assert f(None, 0x1000, 64, 0x2000, 4, 100, 0x3000) == -2
+    assert f(None, 0x1000, 64, 0x2000, 0, 128, 0x3000) == 0
+
+
+def test_ubatch_compression_roundtrip():
+    """UBatch (per-sequence absolute cells, engine.cpp:501-507) -> block tables."""
+    from iian_amd import PagedBatch
+    bs = 16
+    tables = [[5, 9, 2], [7], [3, 11]]
+    lens = [40, 16, 17]
+    seq_cells = [[t[i // bs] * bs + i % bs for i in range(n)] for t, n in zip(tables, lens)]
+    pos = [39, 15, 15, 16]
+    seq_idx = [0, 1, 2, 2]
+    slots = [seq_cells[s][p] for s, p in zip(seq_idx, pos)]
+    b = PagedBatch.from_ubatch(pos, seq_idx, slots, seq_cells, block_size=bs, device="cpu")
+    assert b.block_tables.tolist() == [[5, 9, 2], [7, 0, 0], [3, 11, 0]]
+    assert b.seq_lens.tolist() == lens
+    assert b.query_start_loc.tolist() == [0, 1, 2, 4]
+    assert b.max_query_len == 2
+    assert b.slots.tolist() == slots
+    with pytest.raises(ValueError):
+        PagedBatch.from_ubatch(pos, [0, 2, 1, 2], slots, seq_cells, device="cpu")      # not contiguous
+    bad = [list(c) for c in seq_cells]
+    bad[0][3] += 1
+    with pytest.raises(ValueError):
+        PagedBatch.from_ubatch(pos, seq_idx, slots, bad, device="cpu")                 # not block-structured
+    with pytest.raises(ValueError):
+        PagedBatch.from_ubatch(pos, seq_idx, slots, seq_cells, device="cpu",
+                               seq_cell_pos=[list(range(40)), list(range(16)), [1] * 17])
+
+
+def test_host_wrappers_validate_before_launch():
+    from iian_amd import KVPool, PagedAttnParams, PagedBatch, build_paged_attn
+    pool = KVPool.wrap(torch.zeros((64, 512), dtype=torch.uint8), 256, 1)
+    b = PagedBatch.from_ubatch([3], [0], [3], [[0, 1, 2, 3]], device="cpu")
+    with pytest.raises(ValueError):
+        build_paged_attn(torch.zeros((1, 4, 128), dtype=torch.float16), pool, pool, 2, PagedAttnParams(), b)
+    with pytest.raises(ValueError):
+        build_paged_attn(torch.zeros((1, 4, 64), dtype=torch.float32), pool, pool, 2, PagedAttnParams(), b)
+    with pytest.raises(ValueError):
+        build_paged_attn(torch.zeros((1, 4, 128), dtype=torch.float32).transpose(0, 1), pool, pool, 2,
+                         PagedAttnParams(), b)

@@ -1,0 +1,231 @@
+"""GPU parity: the gfx950 kernels (through the C ABI) against the CPU oracle.
+
+Bars: KV-write placement and Q8_0 values bit-exact; attention max relative
+error per (token, head) row, max|y - r| / max|r|, at most 2e-3 (BASELINE
+north star; fp32 accumulation in both).
+"""
+import zlib
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import F16, F32, Q8_0, make_case, row_rel_err
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+
+@pytest.fixture(scope="module")
+def pa():
+    assert torch.cuda.is_available(), "GPU tests need an MI355X"
+    import iian_amd
+    iian_amd._lib.load()
+    return iian_amd
+
+
+def banner(msg):
+    print(f"\n[gpu] {msg}", flush=True)
+
+
+# ---------------------------------------------------------------- KV write
+
+@pytest.mark.parametrize("type_,n_embd", [(F16, 1024), (F16, 100), (F32, 256), (Q8_0, 1024), (Q8_0, 256)])
+def test_kv_write_bit_exact(pa, oracle, type_, n_embd):
+    banner(f"kv_write type={type_} n_embd={n_embd}")
+    rng = np.random.default_rng(100 + type_ + n_embd)
+    n_cells, T = 4096, 64
+    rb = pa.row_bytes(type_, n_embd)
+    init = rng.integers(0, 256, (n_cells, rb), dtype=np.uint8)
+    rows = rng.standard_normal((T, n_embd)).astype(np.float32)
+    rows[0, :32] = 0.0
+    if n_embd >= 64:
+        rows[1, :32] = 0.0
+        rows[1, 0] = 127.0
+        rows[1, 1:6] = [2.5, -2.5, 0.5, 1.5, 126.5]
+        rows[2] *= 1e-30
+        rows[3] *= 3e4
+    slots = rng.choice(n_cells, T, replace=False).astype(np.int64)
+    pool = pa.KVPool.wrap(torch.as_tensor(init).cuda(), n_embd, type_)
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    pa.set_rows(pool, torch.as_tensor(rows).cuda(), torch.as_tensor(slots).cuda(), err)
+    got = pool.data.cpu().numpy()
+    want = init.copy()
+    assert oracle.set_rows(want, rows, slots, type_) == 0
+    assert int(err.item()) == 0
+    assert np.array_equal(got, want)
+
+
+def test_kv_write_out_of_range_slot_is_flagged_not_written(pa):
+    banner("kv_write out-of-range slot")
+    n_cells = 64
+    pool = pa.KVPool(n_cells, 128, F16)
+    rows = torch.ones((3, 128), dtype=torch.float32, device="cuda")
+    slots = torch.tensor([5, 64, -1], dtype=torch.int64, device="cuda")
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    pa.set_rows(pool, rows, slots, err)
+    got = pool.data.cpu().numpy()
+    assert int(err.item()) & 1
+    assert got[5].view(np.float16).tolist() == [1.0] * 128
+    assert not np.delete(got, 5, axis=0).any()
+
+
+def test_dequant_q8_0_bit_exact(pa, oracle):
+    banner("dequant q8_0")
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((256, 1024)).astype(np.float32)
+    x[7] *= 1e-30
+    qb = oracle.quantize_q8_0(x)
+    pool = pa.KVPool.wrap(torch.as_tensor(qb).cuda(), 1024, Q8_0)
+    idx = torch.as_tensor(rng.choice(256, 100, replace=False).astype(np.int64)).cuda()
+    got = pa.dequant_q8_0(pool, idx).cpu().numpy()
+    want = oracle.dequantize_q8_0(qb[idx.cpu().numpy()], 1024)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+# ---------------------------------------------------------------- attention
+
+def to_device(pa, c):
+    k = pa.KVPool.wrap(torch.as_tensor(c.k_pool).cuda(), c.Hkv * c.D, c.k_type)
+    v = pa.KVPool.wrap(torch.as_tensor(c.v_pool).cuda(), c.Hkv * c.D, c.v_type)
+    nq = np.diff(c.qsl)
+    batch = pa.PagedBatch(block_tables=torch.as_tensor(c.bt).cuda(), seq_lens=torch.as_tensor(c.seq_lens).cuda(),
+                          query_start_loc=torch.as_tensor(c.qsl).cuda(), pos=torch.as_tensor(c.pos).cuda(),
+                          slots=torch.zeros(c.T, dtype=torch.int64, device="cuda"), max_query_len=int(nq.max()),
+                          block_size=c.bs)
+    return k, v, batch
+
+
+def gpu_attention(pa, c, err=None):
+    k, v, batch = to_device(pa, c)
+    prm = pa.PagedAttnParams(scale=c.scale, softcap=c.softcap, causal=c.causal, n_swa=c.n_swa)
+    out = pa.build_paged_attn(torch.as_tensor(c.q).cuda(), k, v, c.Hkv, prm, batch, err_flag=err)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def oracle_attention(oracle, c, items=None):
+    return oracle.paged_attention(c.q, c.k_pool, c.v_pool, c.k_type, c.v_type, c.bt, c.seq_lens, c.seq_idx, c.pos,
+                                  c.Hkv, c.D, c.bs, c.scale, softcap=c.softcap, causal=c.causal, n_swa=c.n_swa,
+                                  n_threads=16, items=items)
+
+
+SMALL = {
+    # name: (H, Hkv, D, lens, nq, kwargs)            which kernel
+    "decode_gqa7_d64": (14, 2, 64, [64, 200, 1000, 17, 1], [1, 1, 1, 1, 1], {}),        # decode, 1 tile
+    "decode_gqa4_d128": (32, 8, 128, [513, 77, 2048, 33], [1, 1, 1, 1], {}),            # decode + split-K merge
+    "decode_gqa2_d256": (16, 8, 256, [1500, 40], [1, 1], {}),
+    "decode_long_splits": (8, 2, 128, [9000, 5000], [1, 1], {}),                        # 18 splits
+    "spec_verify_5": (32, 8, 128, [700, 101, 4101], [5, 5, 5], {}),                     # decode, 2 row tiles
+    "spec_verify_d64": (14, 2, 64, [300, 90], [3, 4], {}),
+    "prefill_d128": (32, 8, 128, [600, 200], [512, 70], {}),                            # prefill kernel
+    "prefill_d64": (14, 2, 64, [400], [130], {}),
+    "prefill_d256": (16, 8, 256, [700, 300], [256, 33], {}),
+    "mixed_prefill_decode": (32, 8, 128, [900, 1500, 700, 64], [256, 1, 1, 64], {}),
+    "swa_decode": (16, 8, 256, [3000, 900, 1030], [1, 1, 1], {"n_swa": 1024}),
+    "swa_prefill": (16, 8, 256, [2000, 1200], [256, 100], {"n_swa": 512}),
+    "softcap": (8, 2, 128, [333, 77], [1, 40], {"softcap": 30.0}),
+    "not_causal": (8, 2, 64, [300, 50], [20, 1], {"causal": False}),
+    "prefix_shared": (32, 8, 128, [1200, 1100, 900, 300], [128, 64, 1, 1],
+                      {"shared_blocks": 32, "shared_seqs": 3}),
+    "block_size_32": (8, 2, 128, [500, 61], [1, 40], {"bs": 32}),
+    "random_positions": (8, 2, 64, [300, 200], [6, 40], {"pos_mode": "random"}),
+}
+
+
+@pytest.mark.parametrize("name", sorted(SMALL))
+def test_attention_small_cases(pa, oracle, name):
+    H, Hkv, D, lens, nq, kw = SMALL[name]
+    banner(f"attention {name} H={H} Hkv={Hkv} D={D} lens={lens} nq={nq} {kw}")
+    c = make_case(np.random.default_rng(zlib.crc32(name.encode())), H, Hkv, D, lens, nq,
+                  quantize=oracle.quantize_q8_0, **kw)
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    got = gpu_attention(pa, c, err)
+    want = oracle_attention(oracle, c)
+    e = row_rel_err(got, want)
+    print(f"[gpu] {name}: max row rel err {e.max():.3e}", flush=True)
+    assert int(err.item()) == 0
+    assert np.isfinite(got).all()
+    assert e.max() <= TOL, (name, e.max())
+
+
+def test_attention_all_masked_rows_are_zero(pa, oracle):
+    banner("all-masked rows")
+    rng = np.random.default_rng(42)
+    c = make_case(rng, 8, 2, 128, [100, 40, 0 + 16], [2, 1, 1])
+    c.pos[:] = [-5, -1, -2, 10]          # every cell after the first three queries
+    got = gpu_attention(pa, c)
+    assert np.all(got[:3] == 0.0)
+    assert row_rel_err(got[3:], oracle_attention(oracle, c)[3:]).max() <= TOL
+
+
+def test_attention_bad_block_id_is_clamped_and_flagged(pa):
+    banner("bad block id")
+    rng = np.random.default_rng(43)
+    c = make_case(rng, 8, 2, 128, [100, 40], [1, 1])
+    c.bt[1, 1] = 1 << 30
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    got = gpu_attention(pa, c, err)
+    assert int(err.item()) & 2
+    assert np.isfinite(got).all()
+
+
+def test_attention_block_permutation_invariance_bitwise(pa):
+    banner("block permutation invariance")
+    rng = np.random.default_rng(44)
+    c = make_case(rng, 32, 8, 128, [3000, 700, 64], [1, 5, 1])
+    base = gpu_attention(pa, c)
+    nb = c.k_pool.shape[0] // c.bs
+    perm = rng.permutation(nb)
+    kp, vp = np.empty_like(c.k_pool), np.empty_like(c.v_pool)
+    kp.reshape(nb, -1)[perm] = c.k_pool.reshape(nb, -1)
+    vp.reshape(nb, -1)[perm] = c.v_pool.reshape(nb, -1)
+    c.k_pool, c.v_pool = kp, vp
+    c.bt = np.where(c.bt >= 0, perm[np.maximum(c.bt, 0)], -1).astype(np.int32)
+    assert np.array_equal(base, gpu_attention(pa, c))
+
+
+# ---------------------------------------------------------------- full-size configurations
+
+def config_parity(pa, oracle, name, n_items=None, seed=None):
+    from iian_amd import synth
+    sp = synth.spec(name, seed=seed)
+    banner(f"config {name}: S={len(sp.seq_lens)} T={int(sp.n_q.sum())} H={sp.H} Hkv={sp.Hkv} D={sp.D} "
+           f"n_swa={sp.n_swa} kv_type={sp.kv_type}")
+    w = synth.build(sp, device="cuda")
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    pa.set_rows(w.k_pool, w.k_new, w.batch.slots, err)
+    pa.set_rows(w.v_pool, w.v_new, w.batch.slots, err)
+    out = pa.build_paged_attn(w.q, w.k_pool, w.v_pool, sp.Hkv, w.params, w.batch, err_flag=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    got = out.cpu().numpy()
+    kp, vp = w.k_pool.data.cpu().numpy(), w.v_pool.data.cpu().numpy()
+    items = None
+    if n_items is not None and n_items < w.T * sp.H:
+        items = np.sort(np.random.default_rng(1).choice(w.T * sp.H, n_items, replace=False)).astype(np.int64)
+    want = oracle.paged_attention(w.q.cpu().numpy(), kp, vp, sp.kv_type, sp.kv_type, w.block_tables, sp.seq_lens,
+                                  w.seq_idx, w.pos, sp.Hkv, sp.D, sp.block_size, sp.scale, softcap=sp.softcap,
+                                  causal=True, n_swa=sp.n_swa, n_threads=16, items=items)
+    g, r = got.reshape(-1, sp.D), want.reshape(-1, sp.D)
+    if items is not None:
+        g, r = g[items], r[items]
+    e = row_rel_err(g, r)
+    print(f"[gpu] {name}: rows checked {len(e)}, max row rel err {e.max():.3e}, mean {e.mean():.3e}", flush=True)
+    assert np.isfinite(got).all()
+    assert e.max() <= TOL, (name, e.max())
+    # the KV write of this step landed bit-exactly in both pools
+    rows_k = oracle.f32_to_f16_bits(w.k_new.cpu().numpy()) if sp.kv_type == F16 else oracle.quantize_q8_0(
+        w.k_new.cpu().numpy())
+    assert np.array_equal(kp[w.slots].reshape(rows_k.shape[0], -1).view(np.uint8),
+                          rows_k.view(np.uint8).reshape(rows_k.shape[0], -1))
+
+
+@pytest.mark.parametrize("name,n_items", [
+    ("cfg1", None), ("cfg2", None), ("cfg3", 4096), ("cfg3_p0", 4096),
+    ("cfg5_global_decode", None), ("cfg5_local_decode", None),
+    ("cfg5_global_prefill", 1024), ("cfg5_local_prefill", 1024),
+])
+def test_config_parity(pa, oracle, name, n_items):
+    config_parity(pa, oracle, name, n_items)

@@ -1,0 +1,285 @@
+"""Pins the CPU oracle (oracle/pa_oracle.c) before it is trusted as the checker.
+
+* fp16 conversions against numpy's IEEE float16 casts;
+* Q8_0 quantise/dequantise bit for bit against ggml's own routines compiled
+  from the reference tree (oracle/_ref) and the committed fixtures they wrote;
+* the KV write against its closed form;
+* paged attention against an independent float64 brute force, plus the
+  invariants the reference kernel's construction implies.
+"""
+import zlib
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from helpers import F16, F32, Q8_0, brute_force, make_case, row_rel_err
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def run_oracle(o, c, n_threads=4, items=None, **over):
+    kw = dict(softcap=c.softcap, causal=c.causal, n_swa=c.n_swa)
+    kw.update(over)
+    return o.paged_attention(c.q, c.k_pool, c.v_pool, c.k_type, c.v_type, c.bt, c.seq_lens, c.seq_idx, c.pos,
+                             c.Hkv, c.D, c.bs, c.scale, n_threads=n_threads, items=items, **kw)
+
+
+# ---------------------------------------------------------------- fp16
+
+def test_f16_to_f32_all_halves(oracle):
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = oracle.f16_bits_to_f32(h)
+    ref = h.view(np.float16).astype(np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+def test_f32_to_f16_rne_matches_numpy(oracle):
+    rng = np.random.default_rng(0)
+    bits = rng.integers(0, 2**32, 1 << 20, dtype=np.uint64).astype(np.uint32)
+    # concentrate on the half range, the subnormal range and the rounding boundaries
+    edge = np.concatenate([
+        np.arange(0x33000000, 0x33000000 + 4096), np.arange(0x387fe000, 0x38802000),
+        np.arange(0x477fe000, 0x47802000), [0, 0x80000000, 0x7f800000, 0xff800000, 0x477fefff, 0x477ff000],
+    ]).astype(np.uint32)
+    x = np.concatenate([bits, edge, rng.standard_normal(1 << 16).astype(np.float32).view(np.uint32)]).view(np.float32)
+    got = oracle.f32_to_f16_bits(x)
+    with np.errstate(over="ignore"):
+        ref = x.astype(np.float16).view(np.uint16)
+    nan = np.isnan(x)
+    assert np.array_equal(got[~nan], ref[~nan])
+    assert np.all((got[nan] & 0x7c00) == 0x7c00) and np.all(got[nan] & 0x3ff)
+
+
+# ---------------------------------------------------------------- Q8_0
+
+def q8_inputs(rng):
+    x = rng.standard_normal((64, 256)).astype(np.float32)
+    x[0, :32] = 0.0                                    # all-zero block: d = 0, q = 0
+    x[1, :32] = np.linspace(-3, 3, 32, dtype=np.float32)
+    x[2, :32] = 0.0
+    x[2, 0] = 127.0                                    # amax 127 -> id == 1: exact ties below
+    x[2, 1:8] = [2.5, -2.5, 0.5, 1.5, -0.5, 126.5, 3.5]
+    x[3] *= 1e-30                                      # tiny scales (f16 subnormal d)
+    x[4] *= 1e5                                        # d overflows f16 range
+    return x
+
+
+def test_q8_0_quantiser_tie_is_round_half_even(oracle):
+    x = np.zeros((1, 32), np.float32)
+    x[0, 0] = 127.0
+    x[0, 1:5] = [2.5, -2.5, 0.5, 1.5]
+    qx = oracle.quantize_q8_0(x, "x86")[0, 2:6].view(np.int8)
+    qr = oracle.quantize_q8_0(x, "ref")[0, 2:6].view(np.int8)
+    assert list(qx) == [127, 2, -2, 0]                 # x86 path: _mm256_round_ps nearest-even
+    assert list(qr) == [127, 3, -3, 1]                 # scalar ref path: roundf, ties away from zero
+
+
+def test_q8_0_matches_ggml_reference_build(oracle):
+    ref = oracle.ref_lib()
+    if ref is None:
+        pytest.skip("reference tree not present: oracle/_ref not buildable here (fixtures cover this)")
+    rng = np.random.default_rng(1)
+    x = q8_inputs(rng)
+    for variant, fn in (("x86", ref.ref_quantize_row_q8_0_x86), ("ref", ref.ref_quantize_row_q8_0_scalar)):
+        want = np.zeros((64, 256 // 32 * 34), np.uint8)
+        fn(x.ctypes.data, want.ctypes.data, x.size)
+        got = oracle.quantize_q8_0(x, variant)
+        assert np.array_equal(got, want), variant
+    deq = np.zeros_like(x)
+    qb = oracle.quantize_q8_0(x)
+    ref.ref_dequantize_row_q8_0(qb.ctypes.data, deq.ctypes.data, x.size)
+    assert np.array_equal(oracle.dequantize_q8_0(qb, 256).view(np.uint32), deq.view(np.uint32))
+
+
+def test_q8_0_matches_committed_ggml_fixtures(oracle):
+    f = np.load(GOLDEN / "q8_0_ggml.npz")
+    assert np.array_equal(oracle.quantize_q8_0(f["x"], "x86"), f["q_x86"])
+    assert np.array_equal(oracle.quantize_q8_0(f["x"], "ref"), f["q_ref"])
+    assert np.array_equal(oracle.dequantize_q8_0(f["q_x86"], f["x"].shape[1]).view(np.uint32),
+                          f["deq_x86"].view(np.uint32))
+
+
+def test_q8_0_dequant_closed_form(oracle):
+    rng = np.random.default_rng(2)
+    b = oracle.quantize_q8_0(rng.standard_normal((16, 128)).astype(np.float32))
+    blk = b.reshape(16, 4, 34)
+    d = blk[:, :, :2].copy().view(np.float16).astype(np.float32)
+    want = (blk[:, :, 2:].view(np.int8).astype(np.float32) * d).reshape(16, 128)
+    assert np.array_equal(oracle.dequantize_q8_0(b, 128), want)
+
+
+# ---------------------------------------------------------------- KV write
+
+@pytest.mark.parametrize("type_", [F32, F16, Q8_0])
+def test_set_rows_placement(oracle, type_):
+    rng = np.random.default_rng(3)
+    n_cells, n = 64, 256
+    pool = rng.integers(0, 256, (n_cells, {F32: 4 * n, F16: 2 * n, Q8_0: n // 32 * 34}[type_]), dtype=np.uint8)
+    before = pool.copy()
+    rows = rng.standard_normal((5, n)).astype(np.float32)
+    slots = np.array([7, 3, 63, 0, 20], np.int64)
+    assert oracle.set_rows(pool, rows, slots, type_) == 0
+    untouched = np.setdiff1d(np.arange(n_cells), slots)
+    assert np.array_equal(pool[untouched], before[untouched])
+    if type_ == F32:
+        want = rows.view(np.uint8).reshape(5, -1)
+    elif type_ == F16:
+        want = rows.astype(np.float16).view(np.uint8).reshape(5, -1)
+    else:
+        want = oracle.quantize_q8_0(rows)
+    assert np.array_equal(pool[slots], want)
+
+
+def test_set_rows_rejects_out_of_range_slot(oracle):
+    pool = np.zeros((8, 64), np.uint8)
+    rows = np.ones((2, 32), np.float32)
+    assert oracle.set_rows(pool, rows, np.array([1, 8], np.int64), F16) == -1
+    assert oracle.set_rows(pool, rows, np.array([-1, 2], np.int64), F16) == -1
+    assert not pool.any()
+
+
+# ---------------------------------------------------------------- attention
+
+CASES = {
+    # name: (H, Hkv, D, lens, nq, kwargs)
+    "decode_gqa7_d64": (14, 2, 64, [64, 200, 1000, 17], [1, 1, 1, 1], {}),
+    "decode_gqa4_d128": (32, 8, 128, [513, 77, 1024], [1, 1, 1], {}),
+    "spec_verify_5": (8, 2, 128, [300, 101], [5, 5], {}),
+    "prefill_chunk": (8, 2, 64, [96, 40], [64, 40], {}),
+    "swa_local": (16, 8, 256, [700, 90], [1, 3], {"n_swa": 64}),
+    "softcap": (4, 1, 64, [150], [2], {"softcap": 5.0}),
+    "not_causal": (4, 2, 64, [100, 33], [3, 1], {"causal": False}),
+    "f32_kv": (4, 2, 64, [80], [2], {"k_type": F32}),
+    "mixed_kv_types": (4, 2, 64, [80], [2], {"k_type": F16, "v_type": F32}),
+    "q8_0_kv": (8, 2, 128, [200, 64], [5, 1], {"k_type": Q8_0}),
+    "prefix_shared": (8, 2, 64, [100, 120, 64], [4, 4, 1], {"shared_blocks": 4, "shared_seqs": 3}),
+    "block_size_32": (4, 2, 64, [100, 31], [1, 2], {"bs": 32}),
+}
+
+
+@pytest.mark.parametrize("name", sorted(CASES))
+def test_attention_matches_float64_brute_force(oracle, name):
+    H, Hkv, D, lens, nq, kw = CASES[name]
+    c = make_case(np.random.default_rng(zlib.crc32(name.encode())), H, Hkv, D, lens, nq,
+                  quantize=oracle.quantize_q8_0, **kw)
+    got = run_oracle(oracle, c)
+    ref = brute_force(c)
+    err = row_rel_err(got, ref)
+    assert err.max() < 2e-5, (name, err.max())
+
+
+def test_attention_random_positions_and_masked_rows(oracle):
+    rng = np.random.default_rng(5)
+    c = make_case(rng, 8, 2, 64, [60, 130], [6, 6], pos_mode="random", n_swa=5, quantize=oracle.quantize_q8_0)
+    c.pos[0] = -3                        # every cell is after this query: all masked -> zero row
+    got = run_oracle(oracle, c)
+    assert np.all(got[0] == 0.0)
+    assert row_rel_err(got, brute_force(c)).max() < 2e-5
+
+
+def test_attention_matches_committed_fixture(oracle):
+    f = np.load(GOLDEN / "attn_small.npz")
+    got = oracle.paged_attention(f["q"], f["k_pool"], f["v_pool"], F16, F16, f["bt"], f["seq_lens"], f["seq_idx"],
+                                 f["pos"], int(f["Hkv"]), f["q"].shape[2], 16, float(f["scale"]),
+                                 n_swa=int(f["n_swa"]))
+    assert row_rel_err(got, f["out_f64"]).max() < 2e-5
+
+
+def test_single_cell_returns_v_row(oracle):
+    rng = np.random.default_rng(6)
+    c = make_case(rng, 4, 2, 64, [1], [1])
+    got = run_oracle(oracle, c)
+    cell = int(c.bt[0, 0]) * c.bs
+    v = c.v_pool[cell].view(np.float16).astype(np.float32).reshape(2, 64)
+    assert np.array_equal(got[0, :2], np.repeat(v[:1], 2, 0)) and np.array_equal(got[0, 2:], np.repeat(v[1:], 2, 0))
+
+
+def test_invariants_bitwise(oracle):
+    rng = np.random.default_rng(7)
+    c = make_case(rng, 8, 2, 128, [333, 65, 16], [2, 1, 1])
+    base = run_oracle(oracle, c, n_threads=1)
+    # thread count (paged_attn.cpp:103-106 partitions work, not arithmetic)
+    assert np.array_equal(base, run_oracle(oracle, c, n_threads=7))
+    # physical placement: move every block to another id
+    nb = c.k_pool.shape[0] // c.bs
+    perm = rng.permutation(nb)
+    kp = np.empty_like(c.k_pool)
+    vp = np.empty_like(c.v_pool)
+    kp.reshape(nb, -1)[perm] = c.k_pool.reshape(nb, -1)
+    vp.reshape(nb, -1)[perm] = c.v_pool.reshape(nb, -1)
+    bt2 = np.where(c.bt >= 0, perm[np.maximum(c.bt, 0)], -1).astype(np.int32)
+    moved = oracle.paged_attention(c.q, kp, vp, F16, F16, bt2, c.seq_lens, c.seq_idx, c.pos, c.Hkv, c.D, c.bs,
+                                   c.scale)
+    assert np.array_equal(base, moved)
+    # a window at least as long as the context is full attention
+    assert np.array_equal(base, run_oracle(oracle, c, n_swa=10_000))
+    # subset evaluation computes the same rows
+    items = np.array([0, 5, 17, c.T * c.H - 1], np.int64)
+    sub = run_oracle(oracle, c, items=items)
+    flat_b, flat_s = base.reshape(-1, c.D), sub.reshape(-1, c.D)
+    assert np.array_equal(flat_b[items], flat_s[items])
+
+
+def test_prefix_sharing_equals_private_copies(oracle):
+    rng = np.random.default_rng(8)
+    c = make_case(rng, 8, 2, 64, [100, 90], [3, 2], shared_blocks=4, shared_seqs=2)
+    shared = run_oracle(oracle, c)
+    # give sequence 1 private copies of the 4 shared blocks
+    free = np.setdiff1d(np.arange(c.k_pool.shape[0] // c.bs), c.bt[c.bt >= 0])[:4]
+    kp, vp, bt = c.k_pool.copy(), c.v_pool.copy(), c.bt.copy()
+    for j, b in enumerate(c.bt[1, :4]):
+        kp[free[j] * c.bs:(free[j] + 1) * c.bs] = c.k_pool[b * c.bs:(b + 1) * c.bs]
+        vp[free[j] * c.bs:(free[j] + 1) * c.bs] = c.v_pool[b * c.bs:(b + 1) * c.bs]
+        bt[1, j] = free[j]
+    private = oracle.paged_attention(c.q, kp, vp, F16, F16, bt, c.seq_lens, c.seq_idx, c.pos, c.Hkv, c.D, c.bs,
+                                     c.scale)
+    assert np.array_equal(shared, private)
+
+
+def test_gqa_head_map(oracle):
+    # heads of one group with identical q must give identical rows; another group differs
+    rng = np.random.default_rng(9)
+    c = make_case(rng, 8, 2, 64, [50], [1])
+    c.q[0, 1] = c.q[0, 0]
+    c.q[0, 4] = c.q[0, 0]
+    got = run_oracle(oracle, c)
+    assert np.array_equal(got[0, 0], got[0, 1])
+    assert not np.allclose(got[0, 0], got[0, 4])
+
+
+def test_swa_boundary(oracle):
+    # p1 - p0 >= n_swa is masked: with n_swa = 1 a query attends only its own cell
+    rng = np.random.default_rng(10)
+    c = make_case(rng, 4, 2, 64, [40], [1], n_swa=1)
+    got = run_oracle(oracle, c)
+    cell = int(c.bt[0, 39 // 16]) * 16 + 39 % 16
+    v = c.v_pool[cell].view(np.float16).astype(np.float32).reshape(2, 64)
+    assert np.array_equal(got[0, 0], v[0]) and np.array_equal(got[0, 3], v[1])
+    # the float64 reference agrees for a wider window
+    c2 = make_case(rng, 4, 2, 64, [40], [1], n_swa=7)
+    assert row_rel_err(run_oracle(oracle, c2), brute_force(c2)).max() < 2e-5
+
+
+def test_softcap_closed_form(oracle):
+    # softcap * tanh(s / softcap) with a cap far above |s| is the identity to fp32 precision
+    rng = np.random.default_rng(11)
+    c = make_case(rng, 4, 2, 64, [70], [1])
+    a = run_oracle(oracle, c)
+    b = run_oracle(oracle, c, softcap=1e4)
+    assert np.abs(a - b).max() < 1e-5
+    c.softcap = 0.5
+    assert row_rel_err(run_oracle(oracle, c), brute_force(c)).max() < 2e-5
+
+
+def test_invalid_arguments_rejected(oracle):
+    rng = np.random.default_rng(12)
+    c = make_case(rng, 4, 2, 64, [20], [1])
+    with pytest.raises(ValueError):
+        oracle.paged_attention(c.q, c.k_pool, c.v_pool, F16, F16, c.bt, np.array([10_000], np.int32), c.seq_idx,
+                               c.pos, c.Hkv, c.D, c.bs, c.scale)
+    with pytest.raises(ValueError):
+        oracle.paged_attention(c.q, c.k_pool, c.v_pool, F16, F16, c.bt, c.seq_lens, np.array([3], np.int32),
+                               c.pos, c.Hkv, c.D, c.bs, c.scale)
