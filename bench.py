@@ -25,6 +25,19 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "paged decode attn achieved HBM GB/s (% of peak) + attn tok/s, Llama-3-8B shapes"
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+WORKLOADS = {
+    "cfg1": "Qwen2.5-0.5B paged decode, H14/Hkv2/D64, 8 seqs, ctx U[64,1024], 1024-block f16 pool",
+    "cfg2": "Llama-3-8B paged decode, H32/Hkv8/D128, 64 seqs, ctx log-uniform [512,8192], "
+            "16-token f16 blocks in a 65536-block pool, + KV write of 64 tokens",
+    "cfg3": "Qwen3-8B mixed batch, H32/Hkv8/D128: 4 prefill chunks x 512 over prior U[1024,4096] "
+            "(1024-token shared prefix) + 32 decode tokens, f16 KV",
+    "cfg4": "Llama-3-8B Q8_0 KV, 128 seqs x 4096 prior + 5 spec-verify queries",
+    "cfg5_global_decode": "Gemma3-12B global layer decode, H16/Hkv8/D256, 32 seqs, ctx U[8192,32768]",
+    "cfg5_local_decode": "Gemma3-12B local layer decode (n_swa=1024), H16/Hkv8/D256, 32 seqs",
+    "cfg5_global_prefill": "Gemma3-12B global layer, 256-token prefill chunk per seq, 32 seqs",
+    "cfg5_local_prefill": "Gemma3-12B local layer (n_swa=1024), 256-token prefill chunk per seq, 32 seqs",
+}
 
 
 def log(msg: str) -> None:
@@ -64,6 +77,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="cfg2")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="after the timed steps, run one plain device copy of this many MiB (HBM counter scale)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU's share: this build runs on a single MI355X "
@@ -81,8 +96,9 @@ def main() -> int:
     w = synth.build(sp, device="cuda")
     b_step = synth.algorithmic_bytes(w, include_kv_write=True)
     b_attn = synth.algorithmic_bytes(w, include_kv_write=False)
-    ws = torch.empty(pa.workspace_size(w.T, sp.H, sp.D, w.block_tables.shape[1], sp.block_size),
-                     dtype=torch.uint8, device="cuda")
+    flops = synth.attention_flops(w)
+    mfma_bound = int(sp.n_q.max()) * (sp.H // sp.Hkv) > 32
+    ws = pa.new_workspace(w.T, len(sp.seq_lens), sp.H, sp.Hkv, sp.D, w.block_tables.shape[1], sp.block_size)
     out = torch.empty((w.T, sp.H, sp.D), dtype=torch.float32, device="cuda")
     stream = torch.cuda.current_stream()
 
@@ -122,7 +138,19 @@ def main() -> int:
     torch.cuda.synchronize()
     attn_ms = sum(a.elapsed_time(b) for a, b in ev) / len(ev)
     attn_gbs = b_attn / (attn_ms * 1e-3) / 1e9
-    log(f"attention: {attn_ms * 1e3:.1f} us/launch, {attn_gbs:.0f} GB/s algorithmic")
+    attn_tfs = flops / (attn_ms * 1e-3) / 1e12
+    log(f"attention: {attn_ms * 1e3:.1f} us/launch, {attn_gbs:.0f} GB/s algorithmic, {attn_tfs:.1f} TFLOP/s")
+
+    if args.copy_calibration:
+        # a copy kernel that reads and writes exactly n bytes: its FETCH_SIZE /
+        # WRITE_SIZE under rocprofv3 --pmc scale the counters of the kernels above
+        n = args.copy_calibration << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy calibration: {n} bytes read, {n} bytes written")
 
     value = b_step / (ms_step * 1e-3) / 1e9
     res = {
@@ -139,24 +167,23 @@ def main() -> int:
         "dtype": "f16",
         "data": "synthetic",
         "config": {
-            "workload": f"{args.config}: " + {
-                "cfg2": "Llama-3-8B paged decode, H32/Hkv8/D128, 64 seqs, ctx log-uniform [512,8192], "
-                        "16-token f16 blocks in a 65536-block pool, + KV write of 64 tokens",
-            }.get(args.config, args.config),
+            "workload": f"{args.config}: " + WORKLOADS.get(args.config, args.config),
             "n_seqs": len(sp.seq_lens), "n_tokens": w.T, "sum_ctx": int(sp.seq_lens.sum()),
             "algorithmic_bytes_per_step": b_step,
         },
         "hbm_frac_of_peak": round(value / HBM_PEAK_GBS, 4),
         "attn_tok_per_s": round(w.T / (attn_ms * 1e-3), 1),
         "roofline": {
-            "bound": "hbm",
-            "kernel": "iian_pa_attention (pa_decode_f16_kernel + pa_merge_kernel)",
-            "achieved": round(attn_gbs, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(attn_gbs / HBM_PEAK_GBS, 4),
+            "bound": "mfma" if mfma_bound else "hbm",
+            "kernel": "iian_pa_attention (" + ("pa_prefill_f16_kernel" if mfma_bound else
+                                               "pa_decode_f16_kernel + pa_merge_kernel") + ")",
+            "achieved": round(attn_tfs if mfma_bound else attn_gbs, 1),
+            "peak": MFMA_F16_PEAK_TFLOPS if mfma_bound else HBM_PEAK_GBS,
+            "unit": "TFLOP/s" if mfma_bound else "GB/s",
+            "frac": round(attn_tfs / MFMA_F16_PEAK_TFLOPS if mfma_bound else attn_gbs / HBM_PEAK_GBS, 4),
             "traffic": None,
             "algorithmic_bytes_per_launch": b_attn,
+            "flops_per_launch": flops,
             "avg_launch_us": round(attn_ms * 1e3, 2),
         },
     }

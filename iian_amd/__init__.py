@@ -14,6 +14,7 @@ from .paged_attn import (  # noqa: F401
     PagedBatch,
     build_paged_attn,
     dequant_q8_0,
+    new_workspace,
     paged_attn_supported,
     row_bytes,
     set_rows,

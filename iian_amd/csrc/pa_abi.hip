@@ -13,7 +13,10 @@ namespace {
 using namespace iian_pa;
 
 // Cells a split-K partition of the decode kernel covers before it splits again.
-constexpr int kSplitCells = 512;
+#ifndef PA_SPLIT_CELLS
+#define PA_SPLIT_CELLS 512
+#endif
+constexpr int kSplitCells = PA_SPLIT_CELLS;
 // Sequences with n_q*gqa up to this many rows run through the decode kernel.
 constexpr int kDecodeRowsMax = 32;
 
@@ -21,6 +24,26 @@ int max_splits_for(int32_t max_blocks, int32_t block_size) {
     const int64_t cells = (int64_t) max_blocks * block_size + kTile;
     const int64_t ns = (cells + kSplitCells - 1) / kSplitCells;
     return (int) (ns < 1 ? 1 : ns);
+}
+
+// Workspace: [partial (m, l) T*H*splits*2 f32][partial O T*H*splits*Dv f32],
+// each section 256-byte aligned.
+struct WorkspaceLayout {
+    size_t ml, o, total;
+};
+
+inline size_t align256(size_t v) { return (v + 255) & ~(size_t) 255; }
+
+WorkspaceLayout workspace_layout(int32_t n_tokens, int32_t n_seqs, int32_t n_head, int32_t n_head_kv,
+                                 int32_t head_dim_v, int max_splits) {
+    WorkspaceLayout l;
+    (void) n_seqs;
+    (void) n_head_kv;
+    const size_t rows = (size_t) n_tokens * n_head * max_splits;
+    l.ml = 0;
+    l.o = l.ml + align256(rows * 2 * sizeof(float));
+    l.total = l.o + align256(rows * head_dim_v * sizeof(float));
+    return l;
 }
 
 int log2_exact(int32_t v) {
@@ -79,14 +102,14 @@ int iian_pa_kv_write(void *stream, const float *rows, int64_t n_rows, int64_t ro
     return e == hipSuccess ? IIAN_PA_OK : IIAN_PA_ERR_HIP;
 }
 
-size_t iian_pa_workspace_size(int32_t n_tokens, int32_t n_head, int32_t head_dim_v, int32_t max_blocks,
-                              int32_t block_size) {
-    if (n_tokens < 0 || n_head <= 0 || head_dim_v <= 0 || max_blocks < 0 || block_size <= 0) return 0;
-    const int ms = max_splits_for(max_blocks, block_size);
-    const size_t rows = (size_t) n_tokens * n_head * ms;
-    const size_t o_bytes = (rows * head_dim_v * sizeof(float) + 255) & ~(size_t) 255;
-    const size_t ml_bytes = (rows * 2 * sizeof(float) + 255) & ~(size_t) 255;
-    return o_bytes + ml_bytes + 256;
+size_t iian_pa_workspace_size(int32_t n_tokens, int32_t n_seqs, int32_t n_head, int32_t n_head_kv,
+                              int32_t head_dim_v, int32_t max_blocks, int32_t block_size) {
+    if (n_tokens < 0 || n_seqs < 0 || n_head <= 0 || n_head_kv <= 0 || head_dim_v <= 0 || max_blocks < 0 ||
+        block_size <= 0)
+        return 0;
+    const WorkspaceLayout l = workspace_layout(n_tokens, n_seqs, n_head, n_head_kv, head_dim_v,
+                                               max_splits_for(max_blocks, block_size));
+    return l.total + 256;   // room to align the caller's base to 256 bytes
 }
 
 int iian_pa_attention(void *stream, const float *q, const void *k_pool, const void *v_pool, int type_k, int type_v,
@@ -106,7 +129,8 @@ int iian_pa_attention(void *stream, const float *q, const void *k_pool, const vo
     if (bs_log2 < 3) return IIAN_PA_ERR_UNSUPPORTED;   // the 8-cell groups of a tile must not straddle a block
     if (!iian_pa_supported(type_k, type_v, head_dim, head_dim_v, 0.0f)) return IIAN_PA_ERR_UNSUPPORTED;
     if (((uintptr_t) q | (uintptr_t) k_pool | (uintptr_t) v_pool | (uintptr_t) out) & 15) return IIAN_PA_ERR_ARG;
-    const size_t need = iian_pa_workspace_size(n_tokens, n_head, head_dim_v, max_blocks, block_size);
+    const size_t need =
+        iian_pa_workspace_size(n_tokens, n_seqs, n_head, n_head_kv, head_dim_v, max_blocks, block_size);
     if (!workspace || workspace_bytes < need) return IIAN_PA_ERR_WORKSPACE;
 
     AttnParams p = {};
@@ -140,11 +164,10 @@ int iian_pa_attention(void *stream, const float *q, const void *k_pool, const vo
     p.n_swa = n_swa;
     p.max_splits = max_splits_for(max_blocks, block_size);
     p.split_cells = kSplitCells;
-    const size_t rows = (size_t) n_tokens * n_head * p.max_splits;
-    const size_t o_bytes = (rows * head_dim_v * sizeof(float) + 255) & ~(size_t) 255;
+    const WorkspaceLayout wl = workspace_layout(n_tokens, n_seqs, n_head, n_head_kv, head_dim_v, p.max_splits);
     char *ws = (char *) (((uintptr_t) workspace + 255) & ~(uintptr_t) 255);
-    p.part_o = (float *) ws;
-    p.part_ml = (float *) (ws + o_bytes);
+    p.part_ml = (float *) (ws + wl.ml);
+    p.part_o = (float *) (ws + wl.o);
 
     // Row budget of the decode kernel: one 16-row MFMA tile, or two when that
     // covers every sequence of the call (spec-verify); larger sequences go to

@@ -4,8 +4,7 @@
 // its sequence that maps to the kv head: row r = j*gqa + g for query token j
 // and head g of the GQA group (so the group shares each K/V load), up to 16*NRT
 // rows.  It walks its split's cells in 32-cell tiles straight from the block
-// table (no gather), with the next tile's K/V loads in flight while the current
-// tile is computed:
+// table (no gather):
 //
 //   S^T (32 cells x 16 rows) = K * Q^T     v_mfma_f32_16x16x32_f16, K rows are
 //                                           the A operand: each lane loads 16
@@ -16,8 +15,16 @@
 //                                           operand; V^T B operands are built
 //                                           from 16-byte row loads with v_perm
 //
-// Splits write unnormalised partials (O, m, l); pa_merge combines them with a
-// log-sum-exp merge.  A sequence with a single split writes its output directly.
+// The split's block-table entries are read once into a register (lane i holds
+// logical block first+i) and handed out with lane shuffles, so a tile's loads
+// never wait on a table read.  Loads are single-buffered and phase-pipelined:
+// the next tile's K loads are issued as soon as this tile's QK^T MFMAs have
+// consumed K, its V loads as soon as V has been transposed, so they overlap the
+// softmax and PV work of this tile.
+//
+// Splits write unnormalised partials (O, m, l); pa_merge_kernel combines them
+// with a log-sum-exp merge.  A sequence with a single split writes its output
+// directly.
 // Semantics follow paged_attn_impl (src/iian/paged_attn.cpp:90-146): masks
 // (:124), softcap (:127), all-masked rows -> 0 (:132).
 #include "pa_common.h"
@@ -25,152 +32,99 @@
 
 namespace iian_pa {
 
-// KV storage formats handled by the tile loader.
-enum KvFmt { KV_F16 = 1, KV_Q8_0 = 8 };
-
-template <int D, int KV>
-struct TileRegs;
-
-// f16: K half h, k-step ks -> 8 halves; V: 8 cells x (D/16) halves per lane.
+// K/V are read once per call: non-temporal loads keep them from evicting the
+// block tables and partials.  Measured on MI355X: +5% at D=128 (256-byte head
+// slices), -7% at D=256, so it is chosen per head size.
 template <int D>
-struct TileRegs<D, KV_F16> {
-    static constexpr int KS = D / 32;
-    static constexpr int VW = D / 32;    // dwords of V per cell per lane (D/16 halves)
-    u32x4 k[2][KS];
-    uint32_t v[8][VW];
+struct KvStream {
+    static constexpr bool kNonTemporal = D <= 128;
 };
 
+template <int D, typename T>
+__device__ __forceinline__ T stream_load(const T *ptr) {
+    if constexpr (KvStream<D>::kNonTemporal)
+        return __builtin_nontemporal_load(ptr);
+    else
+        return *ptr;
+}
+
+// Block-table entries of 64 consecutive logical blocks of one sequence, one per lane.
+struct TableWindow {
+    int first;     // logical block held by lane 0
+    int32_t id;    // this lane's physical block id
+};
+
+__device__ __forceinline__ void table_load(const AttnParams &p, int s, int first, int L, TableWindow &tw) {
+    const int lane = threadIdx.x & 63;
+    const int nblk = (L + (1 << p.bs_log2) - 1) >> p.bs_log2;
+    tw.first = first;
+    tw.id = (first + lane < nblk) ? phys_block(p, s, first + lane) : 0;
+}
+
+// Pool row of cell c (c <= L-1) whose 8-cell group starts at grp (grp <= c, same block).
+__device__ __forceinline__ int64_t table_row(const AttnParams &p, const TableWindow &tw, int grp_clamped, int c) {
+    const int blk = __shfl(tw.id, (grp_clamped >> p.bs_log2) - tw.first);
+    return ((int64_t) blk << p.bs_log2) | (c & ((1 << p.bs_log2) - 1));
+}
+
 template <int D>
-__device__ __forceinline__ void load_tile_f16(const AttnParams &p, const SeqWindow &w, int s, int hk, int tile,
-                                              TileRegs<D, KV_F16> &r) {
-    constexpr int KS = D / 32;
+struct KRegs {
+    u32x4 k[2][D / 32];
+};
+template <int D>
+struct VRegs {
+    uint32_t v[8][D / 32];   // 8 cells x (D/16) halves per lane
+};
+
+// K: lane (n, g) loads cells tile + 8*(n/4) + 4h + (n%4), dims 32ks + 8g .. +8
+template <int D>
+__device__ __forceinline__ void load_k(const AttnParams &p, const TableWindow &tw, int L, int hk, int tile,
+                                       KRegs<D> &r) {
+    const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
+    const int last = L - 1;
+    const int grp = min(tile + 8 * (n >> 2), last);
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const int c = min(tile + 8 * (n >> 2) + 4 * h + (n & 3), last);
+        const int64_t row = table_row(p, tw, grp, c);
+        const char *base = p.k_pool + row * p.k_row + (int64_t) hk * D * 2 + g * 16;
+#pragma unroll
+        for (int ks = 0; ks < D / 32; ks++) r.k[h][ks] = stream_load<D>((const u32x4 *) (base + ks * 64));
+    }
+}
+
+// V: lane (n, g) loads cells tile + 8g + e, dims (D/16)*n .. +D/16
+template <int D>
+__device__ __forceinline__ void load_v(const AttnParams &p, const TableWindow &tw, int L, int hk, int tile,
+                                       VRegs<D> &r) {
     constexpr int VW = D / 32;
     const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
-    const int bs_mask = (1 << p.bs_log2) - 1;
-    const int last = w.L - 1;
-    // K: lane (n, g) loads cells tile + 8*(n/4) + 4h + (n%4), dims 32ks + 8g .. +8
-    {
-        const int grp = tile + 8 * (n >> 2);
-        const int blk = phys_block(p, s, min(grp, last) >> p.bs_log2);
+    const int last = L - 1;
+    const int grp = min(tile + 8 * g, last);
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const int c = min(grp + 4 * h + (n & 3), last);
-            const int64_t row = ((int64_t) blk << p.bs_log2) | (c & bs_mask);
-            const char *base = p.k_pool + row * p.k_row + (int64_t) hk * D * 2 + g * 16;
+    for (int e = 0; e < 8; e++) {
+        const int c = min(tile + 8 * g + e, last);
+        const int64_t row = table_row(p, tw, grp, c);
+        const uint32_t *src = (const uint32_t *) (p.v_pool + row * p.v_row + (int64_t) hk * D * 2 + n * (D / 8));
+        if constexpr (VW == 2) {
+            const u32x2 x = stream_load<D>((const u32x2 *) src);
+            r.v[e][0] = x[0];
+            r.v[e][1] = x[1];
+        } else {
 #pragma unroll
-            for (int ks = 0; ks < KS; ks++) r.k[h][ks] = *(const u32x4 *) (base + ks * 64);
-        }
-    }
-    // V: lane (n, g) loads cells tile + 8g + e, dims (D/16)*n .. +D/16
-    {
-        const int grp = tile + 8 * g;
-        const int blk = phys_block(p, s, min(grp, last) >> p.bs_log2);
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const int c = min(grp + e, last);
-            const int64_t row = ((int64_t) blk << p.bs_log2) | (c & bs_mask);
-            const uint32_t *src = (const uint32_t *) (p.v_pool + row * p.v_row + (int64_t) hk * D * 2 + n * (D / 8));
-            if constexpr (VW == 2) {
-                const u32x2 x = *(const u32x2 *) src;
-                r.v[e][0] = x[0]; r.v[e][1] = x[1];
-            } else {
-#pragma unroll
-                for (int i = 0; i < VW; i += 4) {
-                    const u32x4 x = *(const u32x4 *) (src + i);
-                    r.v[e][i] = x[0]; r.v[e][i + 1] = x[1]; r.v[e][i + 2] = x[2]; r.v[e][i + 3] = x[3];
-                }
+            for (int i = 0; i < VW; i += 4) {
+                const u32x4 x = stream_load<D>((const u32x4 *) (src + i));
+                r.v[e][i] = x[0];
+                r.v[e][i + 1] = x[1];
+                r.v[e][i + 2] = x[2];
+                r.v[e][i + 3] = x[3];
             }
         }
     }
 }
 
-// Per-wave running state of the online softmax for NRT row tiles.
 template <int D, int NRT>
-struct DecodeState {
-    static constexpr int DPL = D / 16;
-    f16x8 q[NRT][D / 32];
-    int prow[NRT];
-    float m[NRT];          // running max of row n (log2 units)
-    float l[NRT];          // partial sum over this lane's cells
-    f32x4 o[NRT][DPL];     // O rows 4g+i, dims DPL*n + m
-};
-
-template <int D, int NRT>
-__device__ __forceinline__ void compute_tile_f16(const AttnParams &p, const SeqWindow &w, int tile,
-                                                 const TileRegs<D, KV_F16> &r, DecodeState<D, NRT> &st) {
-    constexpr int KS = D / 32;
-    constexpr int DPL = D / 16;
-    const int lane = threadIdx.x & 63, g = lane >> 4;
-    // V^T B operands: MFMA m takes dim DPL*n + m of cells 8g .. 8g+7
-    u32x4 vb[DPL];
-#pragma unroll
-    for (int m = 0; m < DPL; m++) {
-        const uint32_t sel = (m & 1) ? 0x07060302u : 0x05040100u;
-#pragma unroll
-        for (int wi = 0; wi < 4; wi++) vb[m][wi] = __builtin_amdgcn_perm(r.v[2 * wi + 1][m >> 1], r.v[2 * wi][m >> 1], sel);
-    }
-    const bool full = tile + kTile <= w.L && (!p.causal || tile + kTile - 1 <= w.pmin) &&
-                      (p.n_swa <= 0 || w.pmax - tile < p.n_swa);
-#pragma unroll
-    for (int rt = 0; rt < NRT; rt++) {
-        float sv[8];
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int ks = 0; ks < KS; ks++)
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, r.k[h][ks]), st.q[rt][ks], acc, 0, 0, 0);
-#pragma unroll
-            for (int i = 0; i < 4; i++) sv[4 * h + i] = acc[i];
-        }
-        if (p.softcap > 0.f) {
-#pragma unroll
-            for (int e = 0; e < 8; e++) sv[e] = p.softcap * tanhf(sv[e] * p.softcap_inv) * kLog2e;
-        }
-        if (!full) {
-#pragma unroll
-            for (int e = 0; e < 8; e++)
-                if (cell_masked(tile + 8 * g + e, w.L, st.prow[rt], p.causal, p.n_swa)) sv[e] = -INFINITY;
-        }
-        float mt = sv[0];
-#pragma unroll
-        for (int e = 1; e < 8; e++) mt = fmaxf(mt, sv[e]);
-        mt = wave_max(mt);
-        const float mnew = fmaxf(st.m[rt], mt);
-        float alpha = 1.f;
-        float pv[8];
-        if (mnew == -INFINITY) {
-#pragma unroll
-            for (int e = 0; e < 8; e++) pv[e] = 0.f;
-        } else {
-            alpha = __builtin_amdgcn_exp2f(st.m[rt] - mnew);
-#pragma unroll
-            for (int e = 0; e < 8; e++) pv[e] = __builtin_amdgcn_exp2f(sv[e] - mnew);
-        }
-        st.m[rt] = mnew;
-        float ps = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; e++) ps += pv[e];
-        st.l[rt] = st.l[rt] * alpha + ps;
-        // rescale O rows 4g+i by their row's alpha (held by lane 4g+i)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float a = __shfl(alpha, 4 * g + i);
-#pragma unroll
-            for (int m = 0; m < DPL; m++) st.o[rt][m][i] *= a;
-        }
-        u32x4 pa;
-#pragma unroll
-        for (int wi = 0; wi < 4; wi++) pa[wi] = pack_f16x2(pv[2 * wi], pv[2 * wi + 1]);
-        const f16x8 pah = __builtin_bit_cast(f16x8, pa);
-#pragma unroll
-        for (int m = 0; m < DPL; m++)
-            st.o[rt][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pah, __builtin_bit_cast(f16x8, vb[m]), st.o[rt][m], 0, 0, 0);
-    }
-}
-
-template <int D, int NRT>
-__global__ __launch_bounds__(64) void pa_decode_f16_kernel(AttnParams p) {
+__global__ __launch_bounds__(64, (D * NRT <= 128) ? 2 : 1) void pa_decode_f16_kernel(AttnParams p) {
     constexpr int KS = D / 32;
     constexpr int DPL = D / 16;
     const int split = blockIdx.x, hk = blockIdx.y, s = blockIdx.z;
@@ -179,15 +133,24 @@ __global__ __launch_bounds__(64) void pa_decode_f16_kernel(AttnParams p) {
     seq_window(p, s, w);
     const int M = w.nq * p.gqa;
     if (w.nq <= 0 || M > p.decode_rows || split >= w.nsplit) return;
+    const int cb = w.c_lo + split * w.chunk;
+    const int ce = min(w.c_hi, cb + w.chunk);
 
-    DecodeState<D, NRT> st;
+    TableWindow tw;
+    if (cb < ce) table_load(p, s, cb >> p.bs_log2, w.L, tw);
+
+    // Q^T B operands (f16, pre-scaled), row positions, running state
+    f16x8 q[NRT][KS];
+    int prow[NRT];
+    float m_run[NRT], l_run[NRT];
+    f32x4 o[NRT][DPL];
 #pragma unroll
     for (int rt = 0; rt < NRT; rt++) {
         const int r = rt * 16 + n;
-        st.prow[rt] = w.pmax;
+        prow[rt] = w.pmax;
         if (r < M) {
             const int t = w.q0 + r / p.gqa, h = hk * p.gqa + r % p.gqa;
-            st.prow[rt] = p.pos[t];
+            prow[rt] = p.pos[t];
             const float *qp = p.q + ((int64_t) t * p.H + h) * D + 8 * g;
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) {
@@ -195,39 +158,119 @@ __global__ __launch_bounds__(64) void pa_decode_f16_kernel(AttnParams p) {
                 const float4 b = *(const float4 *) (qp + 32 * ks + 4);
                 const u32x4 u = {pack_f16x2(a.x * p.qscale, a.y * p.qscale), pack_f16x2(a.z * p.qscale, a.w * p.qscale),
                                  pack_f16x2(b.x * p.qscale, b.y * p.qscale), pack_f16x2(b.z * p.qscale, b.w * p.qscale)};
-                st.q[rt][ks] = __builtin_bit_cast(f16x8, u);
+                q[rt][ks] = __builtin_bit_cast(f16x8, u);
             }
         } else {
 #pragma unroll
-            for (int ks = 0; ks < KS; ks++) st.q[rt][ks] = __builtin_bit_cast(f16x8, u32x4{0u, 0u, 0u, 0u});
+            for (int ks = 0; ks < KS; ks++) q[rt][ks] = __builtin_bit_cast(f16x8, u32x4{0u, 0u, 0u, 0u});
         }
-        st.m[rt] = -INFINITY;
-        st.l[rt] = 0.f;
+        m_run[rt] = -INFINITY;
+        l_run[rt] = 0.f;
 #pragma unroll
-        for (int m = 0; m < DPL; m++) st.o[rt][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int m = 0; m < DPL; m++) o[rt][m] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
-    const int cb = w.c_lo + split * w.chunk;
-    const int ce = min(w.c_hi, cb + w.chunk);
     if (cb < ce) {
-        TileRegs<D, KV_F16> ra, rb;
-        int tile = cb;
-        load_tile_f16<D>(p, w, s, hk, tile, ra);
-        while (true) {
-            if (tile + kTile < ce) load_tile_f16<D>(p, w, s, hk, tile + kTile, rb);
-            compute_tile_f16<D, NRT>(p, w, tile, ra, st);
-            tile += kTile;
-            if (tile >= ce) break;
-            if (tile + kTile < ce) load_tile_f16<D>(p, w, s, hk, tile + kTile, ra);
-            compute_tile_f16<D, NRT>(p, w, tile, rb, st);
-            tile += kTile;
-            if (tile >= ce) break;
+        KRegs<D> kr;
+        VRegs<D> vr;
+        load_k<D>(p, tw, w.L, hk, cb, kr);
+        load_v<D>(p, tw, w.L, hk, cb, vr);
+        for (int tile = cb; tile < ce; tile += kTile) {
+            const int next = tile + kTile;
+            const bool has_next = next < ce;
+            if (has_next && ((min(next + kTile - 1, w.L - 1) >> p.bs_log2) - tw.first) >= 64)
+                table_load(p, s, next >> p.bs_log2, w.L, tw);   // splits longer than 64 blocks
+
+            // S^T = K Q^T for every row tile
+            f32x4 sacc[NRT][2];
+#pragma unroll
+            for (int rt = 0; rt < NRT; rt++)
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int ks = 0; ks < KS; ks++)
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, kr.k[h][ks]), q[rt][ks],
+                                                                     acc, 0, 0, 0);
+                    sacc[rt][h] = acc;
+                }
+            if (has_next) load_k<D>(p, tw, w.L, hk, next, kr);
+
+            // online softmax; P becomes the A operand of PV
+            const bool full = tile + kTile <= w.L && (!p.causal || tile + kTile - 1 <= w.pmin) &&
+                              (p.n_swa <= 0 || w.pmax - tile < p.n_swa);
+            f16x8 pa[NRT];
+#pragma unroll
+            for (int rt = 0; rt < NRT; rt++) {
+                float sv[8];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    sv[i] = sacc[rt][0][i];
+                    sv[4 + i] = sacc[rt][1][i];
+                }
+                if (p.softcap > 0.f) {
+#pragma unroll
+                    for (int e = 0; e < 8; e++) sv[e] = p.softcap * tanhf(sv[e] * p.softcap_inv) * kLog2e;
+                }
+                if (!full) {
+#pragma unroll
+                    for (int e = 0; e < 8; e++)
+                        if (cell_masked(tile + 8 * g + e, w.L, prow[rt], p.causal, p.n_swa)) sv[e] = -INFINITY;
+                }
+                float mt = sv[0];
+#pragma unroll
+                for (int e = 1; e < 8; e++) mt = fmaxf(mt, sv[e]);
+                mt = wave_max(mt);
+                const float mnew = fmaxf(m_run[rt], mt);
+                float alpha = 1.f;
+                float pv[8];
+                if (mnew == -INFINITY) {
+#pragma unroll
+                    for (int e = 0; e < 8; e++) pv[e] = 0.f;
+                } else {
+                    alpha = __builtin_amdgcn_exp2f(m_run[rt] - mnew);
+#pragma unroll
+                    for (int e = 0; e < 8; e++) pv[e] = __builtin_amdgcn_exp2f(sv[e] - mnew);
+                }
+                m_run[rt] = mnew;
+                float ps = 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; e++) ps += pv[e];
+                l_run[rt] = l_run[rt] * alpha + ps;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float a = __shfl(alpha, 4 * g + i);   // alpha of O row 4g+i
+#pragma unroll
+                    for (int m = 0; m < DPL; m++) o[rt][m][i] *= a;
+                }
+                u32x4 pk;
+#pragma unroll
+                for (int wi = 0; wi < 4; wi++) pk[wi] = pack_f16x2(pv[2 * wi], pv[2 * wi + 1]);
+                pa[rt] = __builtin_bit_cast(f16x8, pk);
+            }
+
+            // V^T B operands: MFMA m takes dim DPL*n + m of cells 8g .. 8g+7
+            u32x4 vb[DPL];
+#pragma unroll
+            for (int m = 0; m < DPL; m++) {
+                const uint32_t sel = (m & 1) ? 0x07060302u : 0x05040100u;
+#pragma unroll
+                for (int wi = 0; wi < 4; wi++)
+                    vb[m][wi] = __builtin_amdgcn_perm(vr.v[2 * wi + 1][m >> 1], vr.v[2 * wi][m >> 1], sel);
+            }
+            if (has_next) load_v<D>(p, tw, w.L, hk, next, vr);
+#pragma unroll
+            for (int m = 0; m < DPL; m++)
+#pragma unroll
+                for (int rt = 0; rt < NRT; rt++)
+                    o[rt][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[rt], __builtin_bit_cast(f16x8, vb[m]),
+                                                                      o[rt][m], 0, 0, 0);
         }
     }
 
 #pragma unroll
     for (int rt = 0; rt < NRT; rt++) {
-        float l = st.l[rt];
+        float l = l_run[rt];
         l += __shfl_xor(l, 16);
         l += __shfl_xor(l, 32);
         if (w.nsplit == 1) {
@@ -241,8 +284,8 @@ __global__ __launch_bounds__(64) void pa_decode_f16_kernel(AttnParams p) {
                     float *op = p.out + ((int64_t) t * p.H + h) * D + DPL * n;
 #pragma unroll
                     for (int m = 0; m < DPL; m += 4)
-                        *(float4 *) (op + m) = make_float4(st.o[rt][m][i] * inv, st.o[rt][m + 1][i] * inv,
-                                                           st.o[rt][m + 2][i] * inv, st.o[rt][m + 3][i] * inv);
+                        *(float4 *) (op + m) = make_float4(o[rt][m][i] * inv, o[rt][m + 1][i] * inv,
+                                                           o[rt][m + 2][i] * inv, o[rt][m + 3][i] * inv);
                 }
             }
         } else {
@@ -254,53 +297,66 @@ __global__ __launch_bounds__(64) void pa_decode_f16_kernel(AttnParams p) {
                     float *op = p.part_o + (((int64_t) t * p.H + h) * p.max_splits + split) * D + DPL * n;
 #pragma unroll
                     for (int m = 0; m < DPL; m += 4)
-                        *(float4 *) (op + m) = make_float4(st.o[rt][m][i], st.o[rt][m + 1][i], st.o[rt][m + 2][i], st.o[rt][m + 3][i]);
+                        *(float4 *) (op + m) = make_float4(o[rt][m][i], o[rt][m + 1][i], o[rt][m + 2][i], o[rt][m + 3][i]);
                 }
             }
             const int r = rt * 16 + n;
             if (g == 0 && r < M) {
                 const int t = w.q0 + r / p.gqa, h = hk * p.gqa + r % p.gqa;
                 float *mp = p.part_ml + (((int64_t) t * p.H + h) * p.max_splits + split) * 2;
-                *(float2 *) mp = make_float2(st.m[rt], l);
+                *(float2 *) mp = make_float2(m_run[rt], l);
             }
         }
     }
 }
 
-// Log-sum-exp merge of the split-K partials: one wave per (sequence, kv head).
+// Log-sum-exp merge of the split-K partials, one wave per (row, kv head,
+// sequence): out = sum_i 2^(m_i - m) O_i / sum_i 2^(m_i - m) l_i with
+// m = max_i m_i.  A separate launch: the kernel boundary is what makes the
+// partials written on other XCDs visible (their L2s are not coherent within a
+// launch, and a device-scope fence per split costs an L2 write-back).
 template <int D>
 __global__ __launch_bounds__(64) void pa_merge_kernel(AttnParams p) {
     constexpr int DL = D / 64;   // dims per lane
-    const int hk = blockIdx.y, s = blockIdx.z;
+    const int r = blockIdx.x, hk = blockIdx.y, s = blockIdx.z;
     const int lane = threadIdx.x;
     SeqWindow w;
     seq_window(p, s, w);
     const int M = w.nq * p.gqa;
-    if (w.nq <= 0 || M > p.decode_rows || w.nsplit == 1) return;
-    for (int r = 0; r < M; r++) {
-        const int t = w.q0 + r / p.gqa, h = hk * p.gqa + r % p.gqa;
-        const int64_t base = ((int64_t) t * p.H + h) * p.max_splits;
-        float mx = -INFINITY;
-        for (int sp = 0; sp < w.nsplit; sp++) mx = fmaxf(mx, p.part_ml[(base + sp) * 2]);
-        float acc[DL];
+    if (w.nq <= 0 || M > p.decode_rows || w.nsplit == 1 || r >= M) return;
+    const int t = w.q0 + r / p.gqa, h = hk * p.gqa + r % p.gqa;
+    const int64_t base = ((int64_t) t * p.H + h) * p.max_splits;
+    float mx = -INFINITY;
+    for (int sp = lane; sp < w.nsplit; sp += 64) mx = fmaxf(mx, p.part_ml[(base + sp) * 2]);
 #pragma unroll
-        for (int i = 0; i < DL; i++) acc[i] = 0.f;
-        float lsum = 0.f;
-        if (mx != -INFINITY) {
-            for (int sp = 0; sp < w.nsplit; sp++) {
-                const float2 ml = *(const float2 *) (p.part_ml + (base + sp) * 2);
-                const float wgt = __builtin_amdgcn_exp2f(ml.x - mx);   // 0 for an empty split
-                lsum += wgt * ml.y;
-                const float *op = p.part_o + (base + sp) * D + lane * DL;
+    for (int o = 1; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    float acc[DL];
+#pragma unroll
+    for (int i = 0; i < DL; i++) acc[i] = 0.f;
+    float lpart = 0.f;
+    if (mx != -INFINITY) {
+        for (int c0 = 0; c0 < w.nsplit; c0 += 64) {
+            const int nc = min(64, w.nsplit - c0);
+            float wl = 0.f;
+            if (lane < nc) {
+                const float2 ml = *(const float2 *) (p.part_ml + (base + c0 + lane) * 2);
+                wl = __builtin_amdgcn_exp2f(ml.x - mx);   // 0 for an empty split
+                lpart += wl * ml.y;
+            }
+            for (int j = 0; j < nc; j++) {
+                const float wgt = __shfl(wl, j);
+                const float *op = p.part_o + (base + c0 + j) * D + lane * DL;
 #pragma unroll
                 for (int i = 0; i < DL; i++) acc[i] += wgt * op[i];
             }
         }
-        const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-        float *out = p.out + ((int64_t) t * p.H + h) * D + lane * DL;
-#pragma unroll
-        for (int i = 0; i < DL; i++) out[i] = acc[i] * inv;
     }
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) lpart += __shfl_xor(lpart, o);
+    const float inv = lpart > 0.f ? 1.f / lpart : 0.f;
+    float *out = p.out + ((int64_t) t * p.H + h) * D + lane * DL;
+#pragma unroll
+    for (int i = 0; i < DL; i++) out[i] = acc[i] * inv;
 }
 
 template <int D, int NRT>
@@ -308,16 +364,13 @@ static hipError_t launch_decode_t(const AttnParams &p, hipStream_t stream) {
     dim3 grid(p.max_splits, p.Hkv, p.S);
     hipLaunchKernelGGL((pa_decode_f16_kernel<D, NRT>), grid, dim3(64), 0, stream, p);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    if (p.max_splits > 1) {
-        hipLaunchKernelGGL((pa_merge_kernel<D>), dim3(1, p.Hkv, p.S), dim3(64), 0, stream, p);
-        e = hipGetLastError();
-    }
-    return e;
+    if (e != hipSuccess || p.max_splits == 1) return e;
+    hipLaunchKernelGGL((pa_merge_kernel<D>), dim3(p.decode_rows, p.Hkv, p.S), dim3(64), 0, stream, p);
+    return hipGetLastError();
 }
 
 hipError_t launch_decode(const AttnParams &p, int head_dim, int kv_type, hipStream_t stream) {
-    if (kv_type != KV_F16) return hipErrorInvalidValue;
+    if (kv_type != 1) return hipErrorInvalidValue;
     const int nrt = p.decode_rows > 16 ? 2 : 1;
     switch (head_dim) {
         case 64: return nrt == 1 ? launch_decode_t<64, 1>(p, stream) : launch_decode_t<64, 2>(p, stream);

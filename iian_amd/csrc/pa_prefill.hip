@@ -51,15 +51,18 @@ __global__ __launch_bounds__(NW * 64) void pa_prefill_f16_kernel(AttnParams p, i
     constexpr int ROWS = NW * NRT * 16;
     __shared__ __attribute__((aligned(16))) char lds[2][2][SH::TILE_BYTES];
 
-    // XCD-aware remap: consecutive logical ids (same kv head / sequence) share an XCD.
-    const int total = n_rb * p.Hkv * p.S;
-    const int nwg = gridDim.x;
+    // XCD-aware mapping: workgroups are dispatched round-robin over the 8 XCDs
+    // (bid % 8).  (sequence, kv head) pairs are dealt round-robin to XCDs and
+    // all row blocks of a pair run on its XCD, so they share K/V through that
+    // XCD's L2, while neighbouring pairs (the ones that carry work when only a
+    // few sequences of a batch are prefill chunks) land on different XCDs.
     const int bid = blockIdx.x;
-    const int logical = (bid & 7) * (nwg >> 3) + (bid >> 3);
-    if (logical >= total) return;
-    const int rb = logical % n_rb;
-    const int hk = (logical / n_rb) % p.Hkv;
-    const int s = logical / (n_rb * p.Hkv);
+    const int slot = bid >> 3;
+    const int pair = (bid & 7) + 8 * (slot / n_rb);
+    const int rb = slot % n_rb;
+    if (pair >= p.S * p.Hkv) return;
+    const int s = pair / p.Hkv;
+    const int hk = pair % p.Hkv;
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, n = lane & 15;
     const int L = p.seq_lens[s];
@@ -273,8 +276,8 @@ template <int D, int NRT, int NW>
 static hipError_t launch_prefill_t(const AttnParams &p, int max_rows, hipStream_t stream) {
     constexpr int ROWS = NW * NRT * 16;
     const int n_rb = (max_rows + ROWS - 1) / ROWS;
-    const int total = n_rb * p.Hkv * p.S;
-    const int nwg = (total + 7) & ~7;
+    const int pairs_per_xcd = (p.S * p.Hkv + 7) / 8;
+    const int nwg = 8 * pairs_per_xcd * n_rb;
     hipLaunchKernelGGL((pa_prefill_f16_kernel<D, NRT, NW>), dim3(nwg), dim3(NW * 64), 0, stream, p, n_rb);
     return hipGetLastError();
 }

@@ -182,8 +182,17 @@ def set_rows(pool: KVPool, rows: torch.Tensor, slots: torch.Tensor, err_flag: Op
     return pool
 
 
-def workspace_size(n_tokens: int, n_head: int, head_dim_v: int, max_blocks: int, block_size: int) -> int:
-    return int(_lib.load().iian_pa_workspace_size(n_tokens, n_head, head_dim_v, max_blocks, block_size))
+def workspace_size(n_tokens: int, n_seqs: int, n_head: int, n_head_kv: int, head_dim_v: int, max_blocks: int,
+                   block_size: int) -> int:
+    return int(_lib.load().iian_pa_workspace_size(n_tokens, n_seqs, n_head, n_head_kv, head_dim_v, max_blocks,
+                                                  block_size))
+
+
+def new_workspace(n_tokens: int, n_seqs: int, n_head: int, n_head_kv: int, head_dim_v: int, max_blocks: int,
+                  block_size: int, device="cuda") -> torch.Tensor:
+    """A workspace for build_paged_attn, reusable across calls on one stream."""
+    n = workspace_size(n_tokens, n_seqs, n_head, n_head_kv, head_dim_v, max_blocks, block_size)
+    return torch.zeros(n, dtype=torch.uint8, device=device)
 
 
 def build_paged_attn(q: torch.Tensor, k_cache: KVPool, v_cache: KVPool, n_head_kv: int,
@@ -191,7 +200,8 @@ def build_paged_attn(q: torch.Tensor, k_cache: KVPool, v_cache: KVPool, n_head_k
                      workspace: Optional[torch.Tensor] = None,
                      err_flag: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Paged attention of q [T, H, D] over the pools (paged_attn.cpp:90-169);
-    returns f32 [T, H, Dv]."""
+    returns f32 [T, H, Dv].  A workspace from new_workspace() may be passed in
+    and reused across calls."""
     if q.dtype != torch.float32 or q.dim() != 3:
         raise ValueError("q must be f32 [n_tokens, n_head, head_dim]")   # paged_attn.cpp:161
     if not q.is_contiguous():
@@ -210,9 +220,11 @@ def build_paged_attn(q: torch.Tensor, k_cache: KVPool, v_cache: KVPool, n_head_k
     if out is None:
         out = torch.empty((T, H, Dv), dtype=torch.float32, device=q.device)
     max_blocks = int(batch.block_tables.shape[1])
-    need = workspace_size(T, H, Dv, max_blocks, batch.block_size)
-    if workspace is None or workspace.numel() < need:
-        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    need = workspace_size(T, batch.n_seqs, H, n_head_kv, Dv, max_blocks, batch.block_size)
+    if workspace is None:
+        workspace = torch.zeros(need, dtype=torch.uint8, device=q.device)
+    elif workspace.numel() < need:
+        raise ValueError(f"workspace holds {workspace.numel()} bytes, {need} needed")
     lib = _lib.load()
     st = lib.iian_pa_attention(_stream(), q.data_ptr(), k_cache.data.data_ptr(), v_cache.data.data_ptr(),
                                k_cache.type, v_cache.type, num_blocks, batch.block_tables.data_ptr(), max_blocks,

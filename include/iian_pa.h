@@ -70,9 +70,13 @@ int iian_pa_kv_write(void *stream, const float *rows, int64_t n_rows, int64_t ro
                      int32_t *err_flag);
 
 /* Bytes of device workspace iian_pa_attention needs for these sizes (split-K
- * partial results).  Returns 0 on invalid arguments. */
-size_t iian_pa_workspace_size(int32_t n_tokens, int32_t n_head, int32_t head_dim_v,
-                              int32_t max_blocks, int32_t block_size);
+ * partial results).  Returns 0 on invalid arguments.  No counterpart in the
+ * reference, whose CPU op keeps its scratch in thread_local vectors
+ * (src/iian/paged_attn.cpp:108-110).  The workspace needs no initialisation and
+ * can be reused by later calls on the same stream; concurrent calls (different
+ * streams) must not share one. */
+size_t iian_pa_workspace_size(int32_t n_tokens, int32_t n_seqs, int32_t n_head, int32_t n_head_kv,
+                              int32_t head_dim_v, int32_t max_blocks, int32_t block_size);
 
 /* Replaces build_paged_attn + paged_attn_op (src/iian/paged_attn.h:29-30,
  * src/iian/paged_attn.cpp:90-169).  For every query token t and head h:

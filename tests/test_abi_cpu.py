@@ -53,11 +53,13 @@ def test_supported_matrix(lib):
 
 def test_workspace_size(lib):
     from iian_amd import workspace_size
-    a = workspace_size(64, 32, 128, 512, 16)
-    b = workspace_size(64, 32, 128, 1024, 16)
-    assert 0 < a < b
-    assert workspace_size(-1, 32, 128, 512, 16) == 0
-    assert workspace_size(0, 32, 128, 512, 16) > 0
+    a = workspace_size(64, 64, 32, 8, 128, 512, 16)
+    b = workspace_size(64, 64, 32, 8, 128, 1024, 16)
+    c = workspace_size(64, 128, 32, 8, 128, 512, 16)
+    assert 0 < a < b and a <= c
+    assert workspace_size(-1, 64, 32, 8, 128, 512, 16) == 0
+    assert workspace_size(64, 64, 32, 0, 128, 512, 16) == 0
+    assert workspace_size(0, 0, 32, 8, 128, 512, 16) > 0
 
 
 def call_attention(lib, **over):

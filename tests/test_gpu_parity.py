@@ -160,6 +160,27 @@ def test_attention_all_masked_rows_are_zero(pa, oracle):
     assert row_rel_err(got[3:], oracle_attention(oracle, c)[3:]).max() <= TOL
 
 
+def test_workspace_reuse_across_calls(pa, oracle):
+    """One workspace serves consecutive calls: three calls (different queries,
+    then a different batch) all match the oracle."""
+    banner("workspace reuse")
+    rng = np.random.default_rng(45)
+    c = make_case(rng, 32, 8, 128, [5000, 700, 3000, 64], [1, 1, 1, 1])
+    k, v, batch = to_device(pa, c)
+    prm = pa.PagedAttnParams(scale=c.scale)
+    ws = pa.new_workspace(64, 8, c.H, c.Hkv, c.D, c.bt.shape[1], c.bs)
+    for it in range(3):
+        if it == 2:
+            c.seq_lens[:] = [4000, 500, 3000, 20]      # shorter: stays inside every block table
+            c.pos[:] = c.seq_lens - 1
+            k, v, batch = to_device(pa, c)
+        c.q = rng.standard_normal(c.q.shape).astype(np.float32)
+        got = pa.build_paged_attn(torch.as_tensor(c.q).cuda(), k, v, c.Hkv, prm, batch, workspace=ws)
+        torch.cuda.synchronize()
+        e = row_rel_err(got.cpu().numpy(), oracle_attention(oracle, c))
+        assert e.max() <= TOL, (it, e.max())
+
+
 def test_attention_bad_block_id_is_clamped_and_flagged(pa):
     banner("bad block id")
     rng = np.random.default_rng(43)
