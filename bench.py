@@ -44,6 +44,16 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def pmc_traffic(config: str):
+    """HBM bytes per attention launch measured with rocprofv3 --pmc FETCH_SIZE /
+    WRITE_SIZE (scaled by a calibration copy), recorded in profiles/."""
+    f = ROOT / "profiles" / "pmc_traffic.json"
+    if not f.exists():
+        return None
+    rec = json.loads(f.read_text()).get(config)
+    return None if rec is None else int(rec["traffic_bytes_per_launch"])
+
+
 def cpu_baseline(w, runs: int = 5):
     """Median wall time of the CPU oracle over the same step (KV write + all
     (token, head) items), using every host core."""
@@ -181,7 +191,7 @@ def main() -> int:
             "peak": MFMA_F16_PEAK_TFLOPS if mfma_bound else HBM_PEAK_GBS,
             "unit": "TFLOP/s" if mfma_bound else "GB/s",
             "frac": round(attn_tfs / MFMA_F16_PEAK_TFLOPS if mfma_bound else attn_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": pmc_traffic(args.config),
             "algorithmic_bytes_per_launch": b_attn,
             "flops_per_launch": flops,
             "avg_launch_us": round(attn_ms * 1e3, 2),
