@@ -84,7 +84,7 @@ const char *iian_pa_status_string(int status) {
 int iian_pa_supported(int type_k, int type_v, int head_dim, int head_dim_v, float max_alibi_bias) {
     if (max_alibi_bias != 0.0f) return 0;
     if (type_k != type_v) return 0;
-    if (type_k != IIAN_PA_TYPE_F16) return 0;
+    if (type_k != IIAN_PA_TYPE_F16 && type_k != IIAN_PA_TYPE_Q8_0) return 0;
     if (head_dim != head_dim_v) return 0;
     return head_dim == 64 || head_dim == 128 || head_dim == 256;
 }
@@ -174,6 +174,8 @@ int iian_pa_attention(void *stream, const float *q, const void *k_pool, const vo
     // the prefill kernel.
     const int max_rows = max_query_len * p.gqa;
     p.decode_rows = (max_rows > 16 && max_rows <= kDecodeRowsMax) ? kDecodeRowsMax : 16;
+    // Q8_0 pools have the decode / spec-verify kernel only (up to 32 rows per kv head)
+    if (type_k == IIAN_PA_TYPE_Q8_0 && max_rows > p.decode_rows) return IIAN_PA_ERR_UNSUPPORTED;
     hipStream_t st = (hipStream_t) stream;
     hipError_t e = launch_decode(p, head_dim, type_k, st);
     if (e != hipSuccess) return IIAN_PA_ERR_HIP;

@@ -115,6 +115,26 @@ __device__ __forceinline__ void seq_window(const AttnParams &p, int s, SeqWindow
     split_plan(hi - lo, p.split_cells, p.max_splits, w.chunk, w.nsplit);
 }
 
+// Block-table entries of 64 consecutive logical blocks of one sequence, one
+// per lane, read once per split and handed out with lane shuffles.
+struct TableWindow {
+    int first;     // logical block held by lane 0
+    int32_t id;    // this lane's physical block id
+};
+
+__device__ __forceinline__ void table_load(const AttnParams &p, int s, int first, int L, TableWindow &tw) {
+    const int lane = threadIdx.x & 63;
+    const int nblk = (L + (1 << p.bs_log2) - 1) >> p.bs_log2;
+    tw.first = first;
+    tw.id = (first + lane < nblk) ? phys_block(p, s, first + lane) : 0;
+}
+
+// Pool row of cell c (c <= L-1) whose 8-cell group starts at grp (grp <= c, same block).
+__device__ __forceinline__ int64_t table_row(const AttnParams &p, const TableWindow &tw, int grp_clamped, int c) {
+    const int blk = __shfl(tw.id, (grp_clamped >> p.bs_log2) - tw.first);
+    return ((int64_t) blk << p.bs_log2) | (c & ((1 << p.bs_log2) - 1));
+}
+
 __device__ __forceinline__ bool cell_masked(int c, int L, int prow, int causal, int n_swa) {
     return c >= L || (causal && c > prow) || (n_swa > 0 && prow - c >= n_swa);
 }

@@ -48,25 +48,6 @@ __device__ __forceinline__ T stream_load(const T *ptr) {
         return *ptr;
 }
 
-// Block-table entries of 64 consecutive logical blocks of one sequence, one per lane.
-struct TableWindow {
-    int first;     // logical block held by lane 0
-    int32_t id;    // this lane's physical block id
-};
-
-__device__ __forceinline__ void table_load(const AttnParams &p, int s, int first, int L, TableWindow &tw) {
-    const int lane = threadIdx.x & 63;
-    const int nblk = (L + (1 << p.bs_log2) - 1) >> p.bs_log2;
-    tw.first = first;
-    tw.id = (first + lane < nblk) ? phys_block(p, s, first + lane) : 0;
-}
-
-// Pool row of cell c (c <= L-1) whose 8-cell group starts at grp (grp <= c, same block).
-__device__ __forceinline__ int64_t table_row(const AttnParams &p, const TableWindow &tw, int grp_clamped, int c) {
-    const int blk = __shfl(tw.id, (grp_clamped >> p.bs_log2) - tw.first);
-    return ((int64_t) blk << p.bs_log2) | (c & ((1 << p.bs_log2) - 1));
-}
-
 template <int D>
 struct KRegs {
     u32x4 k[2][D / 32];
@@ -359,17 +340,28 @@ __global__ __launch_bounds__(64) void pa_merge_kernel(AttnParams p) {
     for (int i = 0; i < DL; i++) out[i] = acc[i] * inv;
 }
 
+hipError_t launch_merge(const AttnParams &p, int head_dim, hipStream_t stream) {
+    if (p.max_splits == 1) return hipSuccess;
+    const dim3 grid(p.decode_rows, p.Hkv, p.S);
+    switch (head_dim) {
+        case 64: hipLaunchKernelGGL((pa_merge_kernel<64>), grid, dim3(64), 0, stream, p); break;
+        case 128: hipLaunchKernelGGL((pa_merge_kernel<128>), grid, dim3(64), 0, stream, p); break;
+        case 256: hipLaunchKernelGGL((pa_merge_kernel<256>), grid, dim3(64), 0, stream, p); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 template <int D, int NRT>
 static hipError_t launch_decode_t(const AttnParams &p, hipStream_t stream) {
     dim3 grid(p.max_splits, p.Hkv, p.S);
     hipLaunchKernelGGL((pa_decode_f16_kernel<D, NRT>), grid, dim3(64), 0, stream, p);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess || p.max_splits == 1) return e;
-    hipLaunchKernelGGL((pa_merge_kernel<D>), dim3(p.decode_rows, p.Hkv, p.S), dim3(64), 0, stream, p);
-    return hipGetLastError();
+    const hipError_t e = hipGetLastError();
+    return e != hipSuccess ? e : launch_merge(p, D, stream);
 }
 
 hipError_t launch_decode(const AttnParams &p, int head_dim, int kv_type, hipStream_t stream) {
+    if (kv_type == 8) return launch_decode_q8(p, head_dim, stream);
     if (kv_type != 1) return hipErrorInvalidValue;
     const int nrt = p.decode_rows > 16 ? 2 : 1;
     switch (head_dim) {

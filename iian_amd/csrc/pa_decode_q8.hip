@@ -1,0 +1,341 @@
+// pa_decode_q8.hip - split-K paged decode / spec-verify attention over ggml Q8_0
+// KV pools for gfx950 (wave64, MFMA f16).
+//
+// Pool rows are the reference's Q8_0 rows (ggml-common.h:251-256): a head
+// slice is D/32 blocks of {f16 d, int8 q[32]} = 34*D/32 bytes, only 2-byte
+// aligned inside the row, so it cannot feed MFMA operands straight from
+// memory.  Each 32-cell tile is therefore staged per wave:
+//
+//   raw load   2 lanes per cell, each loads its half of the cell's K and V head
+//              slices as an aligned dword window (issued one tile ahead)
+//   stage      int8 -> f16 is exact (|q| <= 128): bias to unsigned, v_perm the
+//              byte under 0x64 (the f16 1024 + u), v_pk_add_f16 -1152.  The
+//              f16 rows go to LDS, the block scales d to LDS as f32.
+//   QK^T       one v_mfma_f32_16x16x32_f16 per Q8_0 block (k-step = block),
+//              scaled by the K block's d per cell in fp32 afterwards
+//   PV         V^T operands via ds_read_b64_tr_b16; each PV MFMA covers 16
+//              dims of one block, so the V block scale is folded into P
+//              (per cell, f32 multiply before the f16 conversion of P)
+//
+// So the dequantised value q*d (ggml-quants.c:553-567) enters the arithmetic
+// with q and d exact; rounding happens only where the f16 kernel rounds (q, P).
+// Partials and the split-K merge are shared with pa_decode.hip.
+// Semantics follow paged_attn_impl (src/iian/paged_attn.cpp:90-146) run on the
+// dequantised pool (the reference CPU op reaches Q8_0 KV only that way).
+#include "pa_common.h"
+#include "pa_launch.h"
+
+namespace iian_pa {
+
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4_q8;
+
+template <int D>
+struct Q8Shape {
+    static constexpr int NB = D / 32;                       // Q8_0 blocks per head slice
+    static constexpr int HS = NB * 34;                      // head-slice bytes
+    static constexpr int NBL = NB / 2;                      // blocks staged by one lane (2 lanes per cell)
+    static constexpr int SH_MAX = (NB == 2) ? 2 : 0;        // lane slices start 4-aligned unless NB == 2
+    static constexpr int W = (34 * NBL + SH_MAX + 3) / 4;   // dwords of one lane's load window
+    static constexpr int STRIDE = D * 2 + 16;               // padded LDS row of f16 values (bytes)
+    static constexpr int TILE_BYTES = kTile * STRIDE;
+};
+
+template <int D>
+struct Q8Lds {
+    __attribute__((aligned(16))) char k[Q8Shape<D>::TILE_BYTES];
+    __attribute__((aligned(16))) char v[Q8Shape<D>::TILE_BYTES];
+    __attribute__((aligned(16))) float ks[Q8Shape<D>::NB][kTile];
+    __attribute__((aligned(16))) float vs[Q8Shape<D>::NB][kTile];
+};
+
+// 4 int8 -> 4 exact f16 (two packed pairs).
+__device__ __forceinline__ void i8x4_to_f16(uint32_t x, uint32_t &lo, uint32_t &hi) {
+    const uint32_t u = x ^ 0x80808080u;                                      // q + 128
+    const uint32_t a = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);   // f16 {1024 + u0, 1024 + u1}
+    const uint32_t b = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);   // f16 {1024 + u2, 1024 + u3}
+    const f16x2 bias = {(_Float16) 1152.0f, (_Float16) 1152.0f};
+    lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, a) - bias);
+    hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, b) - bias);
+}
+
+// Raw Q8_0 bytes of one tile: lane l holds blocks [part*NBL, part*NBL + NBL) of
+// cell tile + l/2 (part = l%2), as the aligned dword window that contains them.
+template <int D>
+__device__ __forceinline__ void q8_load_raw(const AttnParams &p, const TableWindow &tw, int L, int hk, int tile,
+                                            uint32_t (&rk)[Q8Shape<D>::W], uint32_t (&rv)[Q8Shape<D>::W]) {
+    using Q = Q8Shape<D>;
+    const int lane = threadIdx.x & 63;
+    const int c = min(tile + (lane >> 1), L - 1);
+    const int64_t row = table_row(p, tw, c, c);
+    const int off = hk * Q::HS + (lane & 1) * (34 * Q::NBL);
+    const int start = off & ~3;
+    const uint32_t *k = (const uint32_t *) (p.k_pool + row * p.k_row + start);
+    const uint32_t *v = (const uint32_t *) (p.v_pool + row * p.v_row + start);
+#pragma unroll
+    for (int i = 0; i < Q::W; i++) rk[i] = __builtin_nontemporal_load(k + i);
+#pragma unroll
+    for (int i = 0; i < Q::W; i++) rv[i] = __builtin_nontemporal_load(v + i);
+}
+
+// Converts a lane's raw window into f16 rows (tile_lds[cell][D]) and f32 block
+// scales (sc[block][cell]).  sh = byte offset of the lane's first block in the
+// window (0, or 2 for the second lane of a cell when D == 64).
+template <int D>
+__device__ __forceinline__ void q8_stage(const uint32_t (&raw)[Q8Shape<D>::W], int sh, char *tile_lds,
+                                         float (*sc)[kTile]) {
+    using Q = Q8Shape<D>;
+    const int lane = threadIdx.x & 63, cell = lane >> 1, part = lane & 1;
+#pragma unroll
+    for (int j = 0; j < Q::NBL; j++) {
+        const int blk = part * Q::NBL + j;
+        uint32_t q32[8];
+        uint32_t dbits;
+        if constexpr (Q::SH_MAX == 0) {
+            // the window starts at the lane's first block: block j's scale at
+            // byte 34j, its quants at 34j+2 (2 mod 4 for even j, 0 mod 4 for odd)
+            const int b0 = 34 * j;
+            const int q0 = 34 * j + 2;
+            dbits = (raw[b0 >> 2] >> (8 * (b0 & 3))) & 0xffffu;
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const int i0 = (q0 >> 2) + k;
+                q32[k] = (q0 & 3) ? __builtin_amdgcn_alignbyte(raw[min(i0 + 1, Q::W - 1)], raw[i0], q0 & 3) : raw[i0];
+            }
+        } else {
+            // D == 64: one block per lane, starting at byte sh (0 or 2) of the window
+            dbits = (raw[0] >> (8 * sh)) & 0xffffu;
+#pragma unroll
+            for (int k = 0; k < 8; k++)
+                q32[k] = sh ? raw[k + 1] : __builtin_amdgcn_alignbyte(raw[k + 1], raw[k], 2);
+        }
+        sc[blk][cell] = (float) __builtin_bit_cast(_Float16, (uint16_t) dbits);
+        u32x4 h[4];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            uint32_t lo, hi;
+            i8x4_to_f16(q32[k], lo, hi);
+            h[k >> 1][2 * (k & 1)] = lo;
+            h[k >> 1][2 * (k & 1) + 1] = hi;
+        }
+        char *dst = tile_lds + cell * Q::STRIDE + blk * 64;
+#pragma unroll
+        for (int k = 0; k < 4; k++) *(u32x4 *) (dst + 16 * k) = h[k];
+    }
+}
+
+__device__ __forceinline__ f16x8 lds_tr_b16x8_q8(const char *p0, const char *p1) {
+    const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_q8 *) (uintptr_t) p0);
+    const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_q8 *) (uintptr_t) p1);
+    typedef short s16x8 __attribute__((ext_vector_type(8)));
+    const s16x8 c = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+    return __builtin_bit_cast(f16x8, c);
+}
+
+template <int D, int NRT>
+__global__ __launch_bounds__(64, (D * NRT <= 128) ? 2 : 1) void pa_decode_q8_kernel(AttnParams p) {
+    using Q = Q8Shape<D>;
+    constexpr int NB = Q::NB, NPV = D / 16, STRIDE = Q::STRIDE;
+    __shared__ Q8Lds<D> lds;
+    const int split = blockIdx.x, hk = blockIdx.y, s = blockIdx.z;
+    const int lane = threadIdx.x, g = lane >> 4, n = lane & 15;
+    SeqWindow w;
+    seq_window(p, s, w);
+    const int M = w.nq * p.gqa;
+    if (w.nq <= 0 || M > p.decode_rows || split >= w.nsplit) return;
+    const int cb = w.c_lo + split * w.chunk;
+    const int ce = min(w.c_hi, cb + w.chunk);
+
+    TableWindow tw;
+    if (cb < ce) table_load(p, s, cb >> p.bs_log2, w.L, tw);
+
+    // Q^T B operands per block (k-step s covers dims 32s .. 32s+31), row positions, state
+    f16x8 q[NRT][NB];
+    int prow[NRT];
+    float m_run[NRT], l_run[NRT];
+    f32x4 o[NRT][NPV];   // O rows 4g+i, dim 16m + n
+#pragma unroll
+    for (int rt = 0; rt < NRT; rt++) {
+        const int r = rt * 16 + n;
+        prow[rt] = w.pmax;
+        if (r < M) {
+            const int t = w.q0 + r / p.gqa, h = hk * p.gqa + r % p.gqa;
+            prow[rt] = p.pos[t];
+            const float *qp = p.q + ((int64_t) t * p.H + h) * D + 8 * g;
+#pragma unroll
+            for (int ks = 0; ks < NB; ks++) {
+                const float4 a = *(const float4 *) (qp + 32 * ks);
+                const float4 b = *(const float4 *) (qp + 32 * ks + 4);
+                const u32x4 u = {pack_f16x2(a.x * p.qscale, a.y * p.qscale), pack_f16x2(a.z * p.qscale, a.w * p.qscale),
+                                 pack_f16x2(b.x * p.qscale, b.y * p.qscale), pack_f16x2(b.z * p.qscale, b.w * p.qscale)};
+                q[rt][ks] = __builtin_bit_cast(f16x8, u);
+            }
+        } else {
+#pragma unroll
+            for (int ks = 0; ks < NB; ks++) q[rt][ks] = __builtin_bit_cast(f16x8, u32x4{0u, 0u, 0u, 0u});
+        }
+        m_run[rt] = -INFINITY;
+        l_run[rt] = 0.f;
+#pragma unroll
+        for (int m = 0; m < NPV; m++) o[rt][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    if (cb < ce) {
+        const int sh = (Q::SH_MAX == 0) ? 0 : ((hk * Q::HS + (lane & 1) * (34 * Q::NBL)) & 3);
+        uint32_t rk[Q::W], rv[Q::W];
+        q8_load_raw<D>(p, tw, w.L, hk, cb, rk, rv);
+        for (int tile = cb; tile < ce; tile += kTile) {
+            const int next = tile + kTile;
+            const bool has_next = next < ce;
+            __syncthreads();   // the previous tile's LDS reads are done
+            q8_stage<D>(rk, sh, lds.k, lds.ks);
+            q8_stage<D>(rv, sh, lds.v, lds.vs);
+            if (has_next && ((min(next + kTile - 1, w.L - 1) >> p.bs_log2) - tw.first) >= 64)
+                table_load(p, s, next >> p.bs_log2, w.L, tw);
+            if (has_next) q8_load_raw<D>(p, tw, w.L, hk, next, rk, rv);
+            __syncthreads();   // staged tile visible to every lane
+
+            // S^T = sum_blocks d_K[cell] * (K_int Q^T)
+            f32x4 sacc[NRT][2];
+#pragma unroll
+            for (int rt = 0; rt < NRT; rt++) sacc[rt][0] = sacc[rt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const int cr = 8 * (n >> 2) + 4 * h + (n & 3);
+#pragma unroll
+                for (int ks = 0; ks < NB; ks++) {
+                    const f16x8 a = *(const f16x8 *) (lds.k + cr * STRIDE + (32 * ks + 8 * g) * 2);
+                    const f32x4 dk = *(const f32x4 *) &lds.ks[ks][8 * g + 4 * h];
+#pragma unroll
+                    for (int rt = 0; rt < NRT; rt++) {
+                        const f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, q[rt][ks], f32x4{0.f, 0.f, 0.f, 0.f},
+                                                                               0, 0, 0);
+#pragma unroll
+                        for (int i = 0; i < 4; i++) sacc[rt][h][i] = fmaf(c[i], dk[i], sacc[rt][h][i]);
+                    }
+                }
+            }
+
+            const bool full = tile + kTile <= w.L && (!p.causal || tile + kTile - 1 <= w.pmin) &&
+                              (p.n_swa <= 0 || w.pmax - tile < p.n_swa);
+            float pv[NRT][8];
+#pragma unroll
+            for (int rt = 0; rt < NRT; rt++) {
+                float sv[8];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    sv[i] = sacc[rt][0][i];
+                    sv[4 + i] = sacc[rt][1][i];
+                }
+                if (p.softcap > 0.f) {
+#pragma unroll
+                    for (int e = 0; e < 8; e++) sv[e] = p.softcap * tanhf(sv[e] * p.softcap_inv) * kLog2e;
+                }
+                if (!full) {
+#pragma unroll
+                    for (int e = 0; e < 8; e++)
+                        if (cell_masked(tile + 8 * g + e, w.L, prow[rt], p.causal, p.n_swa)) sv[e] = -INFINITY;
+                }
+                float mt = sv[0];
+#pragma unroll
+                for (int e = 1; e < 8; e++) mt = fmaxf(mt, sv[e]);
+                mt = wave_max(mt);
+                const float mnew = fmaxf(m_run[rt], mt);
+                float alpha = 1.f;
+                if (mnew == -INFINITY) {
+#pragma unroll
+                    for (int e = 0; e < 8; e++) pv[rt][e] = 0.f;
+                } else {
+                    alpha = __builtin_amdgcn_exp2f(m_run[rt] - mnew);
+#pragma unroll
+                    for (int e = 0; e < 8; e++) pv[rt][e] = __builtin_amdgcn_exp2f(sv[e] - mnew);
+                }
+                m_run[rt] = mnew;
+                float ps = 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; e++) ps += pv[rt][e];
+                l_run[rt] = l_run[rt] * alpha + ps;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float a = __shfl(alpha, 4 * g + i);
+#pragma unroll
+                    for (int m = 0; m < NPV; m++) o[rt][m][i] *= a;
+                }
+            }
+
+            // O += (P * d_V) V_int, one Q8_0 block (two 16-dim MFMAs) at a time
+            const char *vrow = lds.v + (8 * g + (n >> 2)) * STRIDE + 8 * (n & 3);
+#pragma unroll
+            for (int b = 0; b < NB; b++) {
+                const f32x4 d0 = *(const f32x4 *) &lds.vs[b][8 * g];
+                const f32x4 d1 = *(const f32x4 *) &lds.vs[b][8 * g + 4];
+                f16x8 pb[NRT];
+#pragma unroll
+                for (int rt = 0; rt < NRT; rt++) {
+                    const u32x4 pk = {pack_f16x2(pv[rt][0] * d0[0], pv[rt][1] * d0[1]),
+                                      pack_f16x2(pv[rt][2] * d0[2], pv[rt][3] * d0[3]),
+                                      pack_f16x2(pv[rt][4] * d1[0], pv[rt][5] * d1[1]),
+                                      pack_f16x2(pv[rt][6] * d1[2], pv[rt][7] * d1[3])};
+                    pb[rt] = __builtin_bit_cast(f16x8, pk);
+                }
+#pragma unroll
+                for (int mm = 0; mm < 2; mm++) {
+                    const int m = 2 * b + mm;
+                    const f16x8 vb = lds_tr_b16x8_q8(vrow + 32 * m, vrow + 4 * STRIDE + 32 * m);
+#pragma unroll
+                    for (int rt = 0; rt < NRT; rt++)
+                        o[rt][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pb[rt], vb, o[rt][m], 0, 0, 0);
+                }
+            }
+        }
+    }
+
+#pragma unroll
+    for (int rt = 0; rt < NRT; rt++) {
+        float l = l_run[rt];
+        l += __shfl_xor(l, 16);
+        l += __shfl_xor(l, 32);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int r = rt * 16 + 4 * g + i;
+            const float lr = __shfl(l, 4 * g + i);
+            if (r >= M) continue;
+            const int t = w.q0 + r / p.gqa, h = hk * p.gqa + r % p.gqa;
+            if (w.nsplit == 1) {
+                const float inv = lr > 0.f ? 1.f / lr : 0.f;
+                float *op = p.out + ((int64_t) t * p.H + h) * D + n;
+#pragma unroll
+                for (int m = 0; m < NPV; m++) op[16 * m] = o[rt][m][i] * inv;
+            } else {
+                float *op = p.part_o + (((int64_t) t * p.H + h) * p.max_splits + split) * D + n;
+#pragma unroll
+                for (int m = 0; m < NPV; m++) op[16 * m] = o[rt][m][i];
+            }
+        }
+        const int r = rt * 16 + n;
+        if (w.nsplit > 1 && g == 0 && r < M) {
+            const int t = w.q0 + r / p.gqa, h = hk * p.gqa + r % p.gqa;
+            float *mp = p.part_ml + (((int64_t) t * p.H + h) * p.max_splits + split) * 2;
+            *(float2 *) mp = make_float2(m_run[rt], l);
+        }
+    }
+}
+
+template <int D, int NRT>
+static hipError_t launch_q8_t(const AttnParams &p, hipStream_t stream) {
+    hipLaunchKernelGGL((pa_decode_q8_kernel<D, NRT>), dim3(p.max_splits, p.Hkv, p.S), dim3(64), 0, stream, p);
+    const hipError_t e = hipGetLastError();
+    return e != hipSuccess ? e : launch_merge(p, D, stream);
+}
+
+hipError_t launch_decode_q8(const AttnParams &p, int head_dim, hipStream_t stream) {
+    const int nrt = p.decode_rows > 16 ? 2 : 1;
+    switch (head_dim) {
+        case 64: return nrt == 1 ? launch_q8_t<64, 1>(p, stream) : launch_q8_t<64, 2>(p, stream);
+        case 128: return nrt == 1 ? launch_q8_t<128, 1>(p, stream) : launch_q8_t<128, 2>(p, stream);
+        case 256: return nrt == 1 ? launch_q8_t<256, 1>(p, stream) : launch_q8_t<256, 2>(p, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace iian_pa

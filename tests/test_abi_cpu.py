@@ -45,6 +45,8 @@ def test_supported_matrix(lib):
     F32, F16, Q8 = 0, 1, 8
     assert sup(F16, F16, 0.0, 128)
     assert sup(F16, F16, 0.0, 64) and sup(F16, F16, 0.0, 256)
+    assert sup(Q8, Q8, 0.0, 128) and sup(Q8, Q8, 0.0, 64) and sup(Q8, Q8, 0.0, 256)
+    assert not sup(F32, F32, 0.0, 128)          # F32 pools: KV write only
     assert not sup(F16, F16, 8.0, 128)          # ALiBi (paged_attn.cpp:17)
     assert not sup(F16, F32, 0.0, 128)          # mixed K/V types
     assert not sup(F16, F16, 0.0, 96)           # head size without a kernel
@@ -79,7 +81,8 @@ def call_attention(lib, **over):
     ({"q": None}, -1), ({"k": None}, -1), ({"bt": None}, -1), ({"out": None}, -1), ({"pos": None}, -1),
     ({"H": 6, "Hkv": 4}, -2), ({"Hkv": 0}, -2), ({"T": -1}, -2), ({"maxq": 5}, -2), ({"num_blocks": 0}, -2),
     ({"n_swa": -1}, -2), ({"softcap": -1.0}, -2), ({"scale": float("nan")}, -2), ({"q": 0x1004}, -2),
-    ({"tk": 8, "tv": 8}, -3), ({"tk": 0, "tv": 0}, -3), ({"tk": 1, "tv": 0}, -3), ({"D": 96, "Dv": 96}, -3),
+    ({"tk": 8, "tv": 8, "H": 32, "Hkv": 2, "maxq": 4}, -3),   # Q8_0 pools: no prefill kernel (64 rows)
+    ({"tk": 8, "tv": 8, "D": 96, "Dv": 96}, -3), ({"tk": 0, "tv": 0}, -3), ({"tk": 1, "tv": 0}, -3), ({"D": 96, "Dv": 96}, -3),
     ({"bs": 12}, -3), ({"bs": 4}, -3),
     ({"ws": None}, -4), ({"ws_bytes": 16}, -4),
 ])

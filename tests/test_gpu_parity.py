@@ -131,6 +131,16 @@ SMALL = {
                       {"shared_blocks": 32, "shared_seqs": 3}),
     "block_size_32": (8, 2, 128, [500, 61], [1, 40], {"bs": 32}),
     "random_positions": (8, 2, 64, [300, 200], [6, 40], {"pos_mode": "random"}),
+    # Q8_0 pools (decode / spec-verify kernel)
+    "q8_decode_gqa4_d128": (32, 8, 128, [513, 77, 2048, 33], [1, 1, 1, 1], {"k_type": Q8_0}),
+    "q8_spec_verify_5": (32, 8, 128, [700, 101, 4101], [5, 5, 5], {"k_type": Q8_0}),
+    "q8_decode_gqa7_d64": (14, 2, 64, [64, 200, 1000, 17, 1], [1, 1, 1, 1, 1], {"k_type": Q8_0}),
+    "q8_spec_d64": (14, 2, 64, [300, 90], [3, 4], {"k_type": Q8_0}),
+    "q8_decode_gqa2_d256": (16, 8, 256, [1500, 40], [1, 1], {"k_type": Q8_0}),
+    "q8_swa_d256": (16, 8, 256, [3000, 900], [1, 2], {"k_type": Q8_0, "n_swa": 1024}),
+    "q8_long_splits": (8, 2, 128, [9000, 5000], [1, 1], {"k_type": Q8_0}),
+    "q8_block_size_32": (8, 2, 128, [500, 61], [1, 4], {"k_type": Q8_0, "bs": 32}),
+    "q8_softcap": (8, 2, 128, [333, 77], [1, 3], {"k_type": Q8_0, "softcap": 30.0}),
 }
 
 
@@ -244,7 +254,7 @@ def config_parity(pa, oracle, name, n_items=None, seed=None):
 
 
 @pytest.mark.parametrize("name,n_items", [
-    ("cfg1", None), ("cfg2", None), ("cfg3", 4096), ("cfg3_p0", 4096),
+    ("cfg1", None), ("cfg2", None), ("cfg3", 4096), ("cfg3_p0", 4096), ("cfg4", 2048),
     ("cfg5_global_decode", None), ("cfg5_local_decode", None),
     ("cfg5_global_prefill", 1024), ("cfg5_local_prefill", 1024),
 ])
