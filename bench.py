@@ -123,10 +123,17 @@ def main() -> int:
         kv_write()
         attention()
 
-    for _ in range(args.warmup):
+    # untimed warm-up: the W steps asked for, continued until 0.5 s have passed
+    # so the GPU clocks have left their idle state before the timed region
+    n_warm = 0
+    t_warm = time.perf_counter()
+    while n_warm < args.warmup or time.perf_counter() - t_warm < 0.5:
         step()
+        n_warm += 1
+        if n_warm % 16 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
-    log(f"warmup done ({args.warmup} steps)")
+    log(f"warmup done ({n_warm} steps)")
 
     # timed region: exactly K steps, synchronised on both sides
     torch.cuda.synchronize()

@@ -15,6 +15,11 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kTile = 32;   // cells per KV tile (two 16-row MFMA halves)
+// Lazy online-softmax rescale: a row's reference max moves only when a tile
+// max exceeds it by more than this (log2 units), so P stays <= 2^8 in f16.
+constexpr float kRescaleSlack = 8.0f;
+// Sequences with n_q*gqa up to this many rows per kv head run through the decode kernels.
+constexpr int kDecodeRowsMax = 32;
 
 // Everything the attention kernels read, by value (kernel argument segment).
 struct AttnParams {
@@ -26,8 +31,8 @@ struct AttnParams {
     const int32_t *qsl;         // [S+1]
     const int32_t *pos;         // [T]
     float *out;                 // [T][H][Dv]
-    float *part_o;              // [T][H][max_splits][Dv]   split-K partial numerators
-    float *part_ml;             // [T][H][max_splits][2]    (running max in log2 units, sum)
+    float *part_o;              // [rows][max_splits][Dv]   split-K partial numerators
+    float *part_ml;             // [rows][max_splits][2]    (reference max in log2 units, sum)
     int32_t *err;               // nullable error word
     int64_t k_row;              // bytes per K pool row
     int64_t v_row;
@@ -43,7 +48,17 @@ struct AttnParams {
     int32_t max_splits;
     int32_t split_cells;
     int32_t decode_rows;        // sequences with n_q*gqa <= decode_rows use the decode kernel
+    int32_t part_by_seq;        // partial rows are (seq, kv head, row < kDecodeRowsMax), else (token, head)
 };
+
+// First split-K partial record of query row r = j*gqa + g (token t, head h)
+// of sequence s at kv head hk.  Partials are indexed by (token, head) unless
+// the call has more of those than (sequence, kv head, decode row) slots (a
+// batch dominated by prefill tokens, which never use partials).
+__device__ __forceinline__ int64_t part_base(const AttnParams &p, int s, int hk, int r, int t, int h) {
+    const int64_t row = p.part_by_seq ? ((int64_t) s * p.Hkv + hk) * kDecodeRowsMax + r : (int64_t) t * p.H + h;
+    return row * p.max_splits;
+}
 
 __device__ __forceinline__ float wave_max(float v) {
     v = fmaxf(v, __shfl_xor(v, 16));
@@ -142,6 +157,20 @@ __device__ __forceinline__ bool cell_masked(int c, int L, int prow, int causal, 
 __device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
     const _Float16 ha = (_Float16) a, hb = (_Float16) b;
     return (uint32_t) __builtin_bit_cast(uint16_t, ha) | ((uint32_t) __builtin_bit_cast(uint16_t, hb) << 16);
+}
+
+// 8 floats x*s -> an f16 pair (hi, lo) with hi = f16(x*s), lo = f16(x*s - hi),
+// so hi + lo carries x*s to ~2^-22 relative.  A single f16 q has 2^-11
+// relative error, and a score error of |s|*2^-11 becomes visible once the
+// softmax is peaked (|s| of tens); the extra MFMA per k-step over lo keeps the
+// scores at the reference's f32 q precision.
+__device__ __forceinline__ void split_f16x8(const float4 &a, const float4 &b, float s, f16x8 &hi, f16x8 &lo) {
+    const float x[8] = {a.x * s, a.y * s, a.z * s, a.w * s, b.x * s, b.y * s, b.z * s, b.w * s};
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        hi[e] = (_Float16) x[e];
+        lo[e] = (_Float16) (x[e] - (float) hi[e]);
+    }
 }
 
 }  // namespace iian_pa

@@ -120,8 +120,8 @@ __global__ __launch_bounds__(64, (D * NRT <= 128) ? 2 : 1) void pa_decode_f16_ke
     TableWindow tw;
     if (cb < ce) table_load(p, s, cb >> p.bs_log2, w.L, tw);
 
-    // Q^T B operands (f16, pre-scaled), row positions, running state
-    f16x8 q[NRT][KS];
+    // Q^T B operands (pre-scaled f16 hi/lo pairs), row positions, running state
+    f16x8 qh[NRT][KS], ql[NRT][KS];
     int prow[NRT];
     float m_run[NRT], l_run[NRT];
     f32x4 o[NRT][DPL];
@@ -134,16 +134,13 @@ __global__ __launch_bounds__(64, (D * NRT <= 128) ? 2 : 1) void pa_decode_f16_ke
             prow[rt] = p.pos[t];
             const float *qp = p.q + ((int64_t) t * p.H + h) * D + 8 * g;
 #pragma unroll
-            for (int ks = 0; ks < KS; ks++) {
-                const float4 a = *(const float4 *) (qp + 32 * ks);
-                const float4 b = *(const float4 *) (qp + 32 * ks + 4);
-                const u32x4 u = {pack_f16x2(a.x * p.qscale, a.y * p.qscale), pack_f16x2(a.z * p.qscale, a.w * p.qscale),
-                                 pack_f16x2(b.x * p.qscale, b.y * p.qscale), pack_f16x2(b.z * p.qscale, b.w * p.qscale)};
-                q[rt][ks] = __builtin_bit_cast(f16x8, u);
-            }
+            for (int ks = 0; ks < KS; ks++)
+                split_f16x8(*(const float4 *) (qp + 32 * ks), *(const float4 *) (qp + 32 * ks + 4), p.qscale,
+                            qh[rt][ks], ql[rt][ks]);
         } else {
 #pragma unroll
-            for (int ks = 0; ks < KS; ks++) q[rt][ks] = __builtin_bit_cast(f16x8, u32x4{0u, 0u, 0u, 0u});
+            for (int ks = 0; ks < KS; ks++)
+                qh[rt][ks] = ql[rt][ks] = __builtin_bit_cast(f16x8, u32x4{0u, 0u, 0u, 0u});
         }
         m_run[rt] = -INFINITY;
         l_run[rt] = 0.f;
@@ -170,9 +167,11 @@ __global__ __launch_bounds__(64, (D * NRT <= 128) ? 2 : 1) void pa_decode_f16_ke
                 for (int h = 0; h < 2; h++) {
                     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                    for (int ks = 0; ks < KS; ks++)
-                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, kr.k[h][ks]), q[rt][ks],
-                                                                     acc, 0, 0, 0);
+                    for (int ks = 0; ks < KS; ks++) {
+                        const f16x8 a = __builtin_bit_cast(f16x8, kr.k[h][ks]);
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qh[rt][ks], acc, 0, 0, 0);
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ql[rt][ks], acc, 0, 0, 0);
+                    }
                     sacc[rt][h] = acc;
                 }
             if (has_next) load_k<D>(p, tw, w.L, hk, next, kr);
@@ -275,7 +274,7 @@ __global__ __launch_bounds__(64, (D * NRT <= 128) ? 2 : 1) void pa_decode_f16_ke
                 const int r = rt * 16 + 4 * g + i;
                 if (r < M) {
                     const int t = w.q0 + r / p.gqa, h = hk * p.gqa + r % p.gqa;
-                    float *op = p.part_o + (((int64_t) t * p.H + h) * p.max_splits + split) * D + DPL * n;
+                    float *op = p.part_o + (part_base(p, s, hk, r, t, h) + split) * D + DPL * n;
 #pragma unroll
                     for (int m = 0; m < DPL; m += 4)
                         *(float4 *) (op + m) = make_float4(o[rt][m][i], o[rt][m + 1][i], o[rt][m + 2][i], o[rt][m + 3][i]);
@@ -284,7 +283,7 @@ __global__ __launch_bounds__(64, (D * NRT <= 128) ? 2 : 1) void pa_decode_f16_ke
             const int r = rt * 16 + n;
             if (g == 0 && r < M) {
                 const int t = w.q0 + r / p.gqa, h = hk * p.gqa + r % p.gqa;
-                float *mp = p.part_ml + (((int64_t) t * p.H + h) * p.max_splits + split) * 2;
+                float *mp = p.part_ml + (part_base(p, s, hk, r, t, h) + split) * 2;
                 *(float2 *) mp = make_float2(m_run[rt], l);
             }
         }
@@ -306,7 +305,7 @@ __global__ __launch_bounds__(64) void pa_merge_kernel(AttnParams p) {
     const int M = w.nq * p.gqa;
     if (w.nq <= 0 || M > p.decode_rows || w.nsplit == 1 || r >= M) return;
     const int t = w.q0 + r / p.gqa, h = hk * p.gqa + r % p.gqa;
-    const int64_t base = ((int64_t) t * p.H + h) * p.max_splits;
+    const int64_t base = part_base(p, s, hk, r, t, h);
     float mx = -INFINITY;
     for (int sp = lane; sp < w.nsplit; sp += 64) mx = fmaxf(mx, p.part_ml[(base + sp) * 2]);
 #pragma unroll

@@ -4,10 +4,13 @@
 // Pool rows are the reference's Q8_0 rows (ggml-common.h:251-256): a head
 // slice is D/32 blocks of {f16 d, int8 q[32]} = 34*D/32 bytes, only 2-byte
 // aligned inside the row, so it cannot feed MFMA operands straight from
-// memory.  Each 32-cell tile is therefore staged per wave:
+// memory.  A workgroup owns one (split, kv head, sequence) and has one wave per
+// 16-row query tile (NW = 1, or 2 for spec-verify batches of up to 32 rows per
+// kv head).  Each 32-cell tile is staged once per workgroup:
 //
-//   raw load   2 lanes per cell, each loads its half of the cell's K and V head
-//              slices as an aligned dword window (issued one tile ahead)
+//   raw load   2 lanes per cell, each loads its half of the cell's K or V head
+//              slice as an aligned dword window (issued one tile ahead); with
+//              two waves, wave 0 loads K and wave 1 loads V
 //   stage      int8 -> f16 is exact (|q| <= 128): bias to unsigned, v_perm the
 //              byte under 0x64 (the f16 1024 + u), v_pk_add_f16 -1152.  The
 //              f16 rows go to LDS, the block scales d to LDS as f32.
@@ -19,6 +22,13 @@
 //
 // So the dequantised value q*d (ggml-quants.c:553-567) enters the arithmetic
 // with q and d exact; rounding happens only where the f16 kernel rounds (q, P).
+//
+// Memory order: a head slice is 34*D/32 bytes, so the slices of neighbouring
+// kv heads share cache lines.  The workgroups of all kv heads of one (split,
+// sequence) pair are therefore dispatched back to back onto one XCD (workgroup
+// id mod 8 selects the XCD), and the loads are ordinary cached loads, so a
+// shared line comes from HBM once and is then hit in that XCD's L2.
+//
 // Partials and the split-K merge are shared with pa_decode.hip.
 // Semantics follow paged_attn_impl (src/iian/paged_attn.cpp:90-146) run on the
 // dequantised pool (the reference CPU op reaches Q8_0 KV only that way).
@@ -59,23 +69,22 @@ __device__ __forceinline__ void i8x4_to_f16(uint32_t x, uint32_t &lo, uint32_t &
     hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, b) - bias);
 }
 
-// Raw Q8_0 bytes of one tile: lane l holds blocks [part*NBL, part*NBL + NBL) of
-// cell tile + l/2 (part = l%2), as the aligned dword window that contains them.
+// Raw Q8_0 bytes of one tile of one pool: lane l holds blocks [part*NBL,
+// part*NBL + NBL) of cell tile + l/2 (part = l%2), as the aligned dword window
+// that contains them.  The window never leaves the cell's row: it ends at the
+// slice end (NB > 2) or starts at most 2 bytes before the slice (NB == 2).
 template <int D>
-__device__ __forceinline__ void q8_load_raw(const AttnParams &p, const TableWindow &tw, int L, int hk, int tile,
-                                            uint32_t (&rk)[Q8Shape<D>::W], uint32_t (&rv)[Q8Shape<D>::W]) {
+__device__ __forceinline__ void q8_load_raw(const AttnParams &p, const char *pool, int64_t row_bytes,
+                                            const TableWindow &tw, int L, int hk, int tile,
+                                            uint32_t (&raw)[Q8Shape<D>::W]) {
     using Q = Q8Shape<D>;
     const int lane = threadIdx.x & 63;
     const int c = min(tile + (lane >> 1), L - 1);
     const int64_t row = table_row(p, tw, c, c);
     const int off = hk * Q::HS + (lane & 1) * (34 * Q::NBL);
-    const int start = off & ~3;
-    const uint32_t *k = (const uint32_t *) (p.k_pool + row * p.k_row + start);
-    const uint32_t *v = (const uint32_t *) (p.v_pool + row * p.v_row + start);
+    const uint32_t *src = (const uint32_t *) (pool + row * row_bytes + (off & ~3));
 #pragma unroll
-    for (int i = 0; i < Q::W; i++) rk[i] = __builtin_nontemporal_load(k + i);
-#pragma unroll
-    for (int i = 0; i < Q::W; i++) rv[i] = __builtin_nontemporal_load(v + i);
+    for (int i = 0; i < Q::W; i++) raw[i] = src[i];
 }
 
 // Converts a lane's raw window into f16 rows (tile_lds[cell][D]) and f32 block
@@ -132,73 +141,92 @@ __device__ __forceinline__ f16x8 lds_tr_b16x8_q8(const char *p0, const char *p1)
     return __builtin_bit_cast(f16x8, c);
 }
 
-template <int D, int NRT>
-__global__ __launch_bounds__(64, (D * NRT <= 128) ? 2 : 1) void pa_decode_q8_kernel(AttnParams p) {
+// Orders this wave's LDS accesses before every wave's accesses after it
+// (lgkmcnt(0), then s_barrier when the workgroup has several waves).  Unlike
+// __syncthreads it does not wait for the global loads in flight, which are the
+// next tile's prefetch.
+template <int NW>
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0); vmcnt, expcnt not waited
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    if constexpr (NW > 1) __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+template <int D, int NW>
+__global__ __launch_bounds__(64 * NW, (D <= 128) ? 2 : 1) void pa_decode_q8_kernel(AttnParams p) {
     using Q = Q8Shape<D>;
     constexpr int NB = Q::NB, NPV = D / 16, STRIDE = Q::STRIDE;
+    constexpr int NRAW = NW == 1 ? 2 : 1;   // pools one wave stages: K and V, or one of them
     __shared__ Q8Lds<D> lds;
-    const int split = blockIdx.x, hk = blockIdx.y, s = blockIdx.z;
-    const int lane = threadIdx.x, g = lane >> 4, n = lane & 15;
+    // workgroup id -> (kv head, pair = split + max_splits * sequence); see the header comment
+    const int bid = blockIdx.x;
+    const int hk = (bid >> 3) % p.Hkv;
+    const int pair = (bid & 7) + 8 * (bid / (8 * p.Hkv));
+    const int split = pair % p.max_splits, s = pair / p.max_splits;
+    if (s >= p.S) return;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
     SeqWindow w;
     seq_window(p, s, w);
     const int M = w.nq * p.gqa;
-    if (w.nq <= 0 || M > p.decode_rows || split >= w.nsplit) return;
+    if (w.nq <= 0 || M > p.decode_rows || split >= w.nsplit) return;   // uniform over the workgroup
     const int cb = w.c_lo + split * w.chunk;
     const int ce = min(w.c_hi, cb + w.chunk);
+    const bool rows_live = wave * 16 < M;   // this wave's row tile holds query rows
 
     TableWindow tw;
     if (cb < ce) table_load(p, s, cb >> p.bs_log2, w.L, tw);
 
-    // Q^T B operands per block (k-step s covers dims 32s .. 32s+31), row positions, state
-    f16x8 q[NRT][NB];
-    int prow[NRT];
-    float m_run[NRT], l_run[NRT];
-    f32x4 o[NRT][NPV];   // O rows 4g+i, dim 16m + n
+    // Q^T B operands per block (k-step ks covers dims 32ks .. 32ks+31) as f16
+    // hi/lo pairs, row position, state
+    f16x8 qh[NB], ql[NB];
+    const int qr = wave * 16 + n;
+    int prow = w.pmax;
+    if (qr < M) {
+        const int t = w.q0 + qr / p.gqa, h = hk * p.gqa + qr % p.gqa;
+        prow = p.pos[t];
+        const float *qp = p.q + ((int64_t) t * p.H + h) * D + 8 * g;
 #pragma unroll
-    for (int rt = 0; rt < NRT; rt++) {
-        const int r = rt * 16 + n;
-        prow[rt] = w.pmax;
-        if (r < M) {
-            const int t = w.q0 + r / p.gqa, h = hk * p.gqa + r % p.gqa;
-            prow[rt] = p.pos[t];
-            const float *qp = p.q + ((int64_t) t * p.H + h) * D + 8 * g;
+        for (int ks = 0; ks < NB; ks++)
+            split_f16x8(*(const float4 *) (qp + 32 * ks), *(const float4 *) (qp + 32 * ks + 4), p.qscale, qh[ks],
+                        ql[ks]);
+    } else {
 #pragma unroll
-            for (int ks = 0; ks < NB; ks++) {
-                const float4 a = *(const float4 *) (qp + 32 * ks);
-                const float4 b = *(const float4 *) (qp + 32 * ks + 4);
-                const u32x4 u = {pack_f16x2(a.x * p.qscale, a.y * p.qscale), pack_f16x2(a.z * p.qscale, a.w * p.qscale),
-                                 pack_f16x2(b.x * p.qscale, b.y * p.qscale), pack_f16x2(b.z * p.qscale, b.w * p.qscale)};
-                q[rt][ks] = __builtin_bit_cast(f16x8, u);
-            }
-        } else {
-#pragma unroll
-            for (int ks = 0; ks < NB; ks++) q[rt][ks] = __builtin_bit_cast(f16x8, u32x4{0u, 0u, 0u, 0u});
-        }
-        m_run[rt] = -INFINITY;
-        l_run[rt] = 0.f;
-#pragma unroll
-        for (int m = 0; m < NPV; m++) o[rt][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int ks = 0; ks < NB; ks++) qh[ks] = ql[ks] = __builtin_bit_cast(f16x8, u32x4{0u, 0u, 0u, 0u});
     }
+    float m_run = -INFINITY, l_run = 0.f;   // m_run: reference max (log2 units) of O and l
+    f32x4 o[NPV];                           // O rows 4g+i, dim 16m + n
+#pragma unroll
+    for (int m = 0; m < NPV; m++) o[m] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     if (cb < ce) {
+        const bool stage_k = NW == 1 || wave == 0;
+        const char *pool0 = stage_k ? p.k_pool : p.v_pool;
+        const int64_t row0 = stage_k ? p.k_row : p.v_row;
+        char *dst0 = stage_k ? lds.k : lds.v;
+        float(*sc0)[kTile] = stage_k ? lds.ks : lds.vs;
         const int sh = (Q::SH_MAX == 0) ? 0 : ((hk * Q::HS + (lane & 1) * (34 * Q::NBL)) & 3);
-        uint32_t rk[Q::W], rv[Q::W];
-        q8_load_raw<D>(p, tw, w.L, hk, cb, rk, rv);
+        uint32_t raw[NRAW][Q::W];
+        q8_load_raw<D>(p, pool0, row0, tw, w.L, hk, cb, raw[0]);
+        if constexpr (NRAW == 2) q8_load_raw<D>(p, p.v_pool, p.v_row, tw, w.L, hk, cb, raw[1]);
         for (int tile = cb; tile < ce; tile += kTile) {
             const int next = tile + kTile;
             const bool has_next = next < ce;
-            __syncthreads();   // the previous tile's LDS reads are done
-            q8_stage<D>(rk, sh, lds.k, lds.ks);
-            q8_stage<D>(rv, sh, lds.v, lds.vs);
+            lds_barrier<NW>();   // every wave is done reading the previous tile
+            q8_stage<D>(raw[0], sh, dst0, sc0);
+            if constexpr (NRAW == 2) q8_stage<D>(raw[1], sh, lds.v, lds.vs);
             if (has_next && ((min(next + kTile - 1, w.L - 1) >> p.bs_log2) - tw.first) >= 64)
                 table_load(p, s, next >> p.bs_log2, w.L, tw);
-            if (has_next) q8_load_raw<D>(p, tw, w.L, hk, next, rk, rv);
-            __syncthreads();   // staged tile visible to every lane
+            if (has_next) {
+                q8_load_raw<D>(p, pool0, row0, tw, w.L, hk, next, raw[0]);
+                if constexpr (NRAW == 2) q8_load_raw<D>(p, p.v_pool, p.v_row, tw, w.L, hk, next, raw[1]);
+            }
+            lds_barrier<NW>();   // the staged tile is visible to every wave
+            if (!rows_live) continue;
 
             // S^T = sum_blocks d_K[cell] * (K_int Q^T)
-            f32x4 sacc[NRT][2];
-#pragma unroll
-            for (int rt = 0; rt < NRT; rt++) sacc[rt][0] = sacc[rt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+            f32x4 sacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
             for (int h = 0; h < 2; h++) {
                 const int cr = 8 * (n >> 2) + 4 * h + (n & 3);
@@ -206,62 +234,60 @@ __global__ __launch_bounds__(64, (D * NRT <= 128) ? 2 : 1) void pa_decode_q8_ker
                 for (int ks = 0; ks < NB; ks++) {
                     const f16x8 a = *(const f16x8 *) (lds.k + cr * STRIDE + (32 * ks + 8 * g) * 2);
                     const f32x4 dk = *(const f32x4 *) &lds.ks[ks][8 * g + 4 * h];
+                    f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qh[ks], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ql[ks], c, 0, 0, 0);
 #pragma unroll
-                    for (int rt = 0; rt < NRT; rt++) {
-                        const f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, q[rt][ks], f32x4{0.f, 0.f, 0.f, 0.f},
-                                                                               0, 0, 0);
-#pragma unroll
-                        for (int i = 0; i < 4; i++) sacc[rt][h][i] = fmaf(c[i], dk[i], sacc[rt][h][i]);
-                    }
+                    for (int i = 0; i < 4; i++) sacc[h][i] = fmaf(c[i], dk[i], sacc[h][i]);
                 }
             }
 
             const bool full = tile + kTile <= w.L && (!p.causal || tile + kTile - 1 <= w.pmin) &&
                               (p.n_swa <= 0 || w.pmax - tile < p.n_swa);
-            float pv[NRT][8];
+            float sv[8];
 #pragma unroll
-            for (int rt = 0; rt < NRT; rt++) {
-                float sv[8];
+            for (int i = 0; i < 4; i++) {
+                sv[i] = sacc[0][i];
+                sv[4 + i] = sacc[1][i];
+            }
+            if (p.softcap > 0.f) {
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    sv[i] = sacc[rt][0][i];
-                    sv[4 + i] = sacc[rt][1][i];
-                }
-                if (p.softcap > 0.f) {
+                for (int e = 0; e < 8; e++) sv[e] = p.softcap * tanhf(sv[e] * p.softcap_inv) * kLog2e;
+            }
+            if (!full) {
 #pragma unroll
-                    for (int e = 0; e < 8; e++) sv[e] = p.softcap * tanhf(sv[e] * p.softcap_inv) * kLog2e;
-                }
-                if (!full) {
+                for (int e = 0; e < 8; e++)
+                    if (cell_masked(tile + 8 * g + e, w.L, prow, p.causal, p.n_swa)) sv[e] = -INFINITY;
+            }
+            float mt = sv[0];
 #pragma unroll
-                    for (int e = 0; e < 8; e++)
-                        if (cell_masked(tile + 8 * g + e, w.L, prow[rt], p.causal, p.n_swa)) sv[e] = -INFINITY;
-                }
-                float mt = sv[0];
-#pragma unroll
-                for (int e = 1; e < 8; e++) mt = fmaxf(mt, sv[e]);
-                mt = wave_max(mt);
-                const float mnew = fmaxf(m_run[rt], mt);
-                float alpha = 1.f;
-                if (mnew == -INFINITY) {
-#pragma unroll
-                    for (int e = 0; e < 8; e++) pv[rt][e] = 0.f;
-                } else {
-                    alpha = __builtin_amdgcn_exp2f(m_run[rt] - mnew);
-#pragma unroll
-                    for (int e = 0; e < 8; e++) pv[rt][e] = __builtin_amdgcn_exp2f(sv[e] - mnew);
-                }
-                m_run[rt] = mnew;
-                float ps = 0.f;
-#pragma unroll
-                for (int e = 0; e < 8; e++) ps += pv[rt][e];
-                l_run[rt] = l_run[rt] * alpha + ps;
+            for (int e = 1; e < 8; e++) mt = fmaxf(mt, sv[e]);
+            mt = wave_max(mt);
+            // Lazy rescale: the reference max only moves when a row's tile max
+            // exceeds it by more than kRescaleSlack, so P <= 2^kRescaleSlack
+            // and O, l are rescaled only on those (rare, wave-uniform) tiles.
+            const bool grow = mt > m_run + kRescaleSlack;
+            if (__builtin_amdgcn_ballot_w64(grow)) {
+                const float mnew = grow ? mt : m_run;
+                const float alpha = grow ? __builtin_amdgcn_exp2f(m_run - mnew) : 1.f;   // 0 when m_run = -inf
+                m_run = mnew;
+                l_run *= alpha;
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const float a = __shfl(alpha, 4 * g + i);
+                    const float a = __shfl(alpha, 4 * g + i);   // alpha of O row 4g+i
 #pragma unroll
-                    for (int m = 0; m < NPV; m++) o[rt][m][i] *= a;
+                    for (int m = 0; m < NPV; m++) o[m][i] *= a;
                 }
             }
+            // a row with m_run = -inf has only masked cells so far: its P is 0
+            const float mref = m_run == -INFINITY ? 0.f : m_run;
+            float pv[8];
+            float ps = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                pv[e] = __builtin_amdgcn_exp2f(sv[e] - mref);
+                ps += pv[e];
+            }
+            l_run += ps;
 
             // O += (P * d_V) V_int, one Q8_0 block (two 16-dim MFMAs) at a time
             const char *vrow = lds.v + (8 * g + (n >> 2)) * STRIDE + 8 * (n & 3);
@@ -269,71 +295,63 @@ __global__ __launch_bounds__(64, (D * NRT <= 128) ? 2 : 1) void pa_decode_q8_ker
             for (int b = 0; b < NB; b++) {
                 const f32x4 d0 = *(const f32x4 *) &lds.vs[b][8 * g];
                 const f32x4 d1 = *(const f32x4 *) &lds.vs[b][8 * g + 4];
-                f16x8 pb[NRT];
-#pragma unroll
-                for (int rt = 0; rt < NRT; rt++) {
-                    const u32x4 pk = {pack_f16x2(pv[rt][0] * d0[0], pv[rt][1] * d0[1]),
-                                      pack_f16x2(pv[rt][2] * d0[2], pv[rt][3] * d0[3]),
-                                      pack_f16x2(pv[rt][4] * d1[0], pv[rt][5] * d1[1]),
-                                      pack_f16x2(pv[rt][6] * d1[2], pv[rt][7] * d1[3])};
-                    pb[rt] = __builtin_bit_cast(f16x8, pk);
-                }
+                const u32x4 pk = {pack_f16x2(pv[0] * d0[0], pv[1] * d0[1]), pack_f16x2(pv[2] * d0[2], pv[3] * d0[3]),
+                                  pack_f16x2(pv[4] * d1[0], pv[5] * d1[1]), pack_f16x2(pv[6] * d1[2], pv[7] * d1[3])};
+                const f16x8 pb = __builtin_bit_cast(f16x8, pk);
 #pragma unroll
                 for (int mm = 0; mm < 2; mm++) {
                     const int m = 2 * b + mm;
                     const f16x8 vb = lds_tr_b16x8_q8(vrow + 32 * m, vrow + 4 * STRIDE + 32 * m);
-#pragma unroll
-                    for (int rt = 0; rt < NRT; rt++)
-                        o[rt][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pb[rt], vb, o[rt][m], 0, 0, 0);
+                    o[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pb, vb, o[m], 0, 0, 0);
                 }
             }
         }
     }
+    if (!rows_live) return;
 
+    float l = l_run;
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
 #pragma unroll
-    for (int rt = 0; rt < NRT; rt++) {
-        float l = l_run[rt];
-        l += __shfl_xor(l, 16);
-        l += __shfl_xor(l, 32);
+    for (int i = 0; i < 4; i++) {
+        const int r = wave * 16 + 4 * g + i;
+        const float lr = __shfl(l, 4 * g + i);
+        if (r >= M) continue;
+        const int t = w.q0 + r / p.gqa, h = hk * p.gqa + r % p.gqa;
+        if (w.nsplit == 1) {
+            const float inv = lr > 0.f ? 1.f / lr : 0.f;
+            float *op = p.out + ((int64_t) t * p.H + h) * D + n;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int r = rt * 16 + 4 * g + i;
-            const float lr = __shfl(l, 4 * g + i);
-            if (r >= M) continue;
-            const int t = w.q0 + r / p.gqa, h = hk * p.gqa + r % p.gqa;
-            if (w.nsplit == 1) {
-                const float inv = lr > 0.f ? 1.f / lr : 0.f;
-                float *op = p.out + ((int64_t) t * p.H + h) * D + n;
+            for (int m = 0; m < NPV; m++) op[16 * m] = o[m][i] * inv;
+        } else {
+            float *op = p.part_o + (part_base(p, s, hk, r, t, h) + split) * D + n;
 #pragma unroll
-                for (int m = 0; m < NPV; m++) op[16 * m] = o[rt][m][i] * inv;
-            } else {
-                float *op = p.part_o + (((int64_t) t * p.H + h) * p.max_splits + split) * D + n;
-#pragma unroll
-                for (int m = 0; m < NPV; m++) op[16 * m] = o[rt][m][i];
-            }
+            for (int m = 0; m < NPV; m++) op[16 * m] = o[m][i];
         }
-        const int r = rt * 16 + n;
-        if (w.nsplit > 1 && g == 0 && r < M) {
-            const int t = w.q0 + r / p.gqa, h = hk * p.gqa + r % p.gqa;
-            float *mp = p.part_ml + (((int64_t) t * p.H + h) * p.max_splits + split) * 2;
-            *(float2 *) mp = make_float2(m_run[rt], l);
-        }
+    }
+    if (w.nsplit > 1 && g == 0 && qr < M) {
+        const int t = w.q0 + qr / p.gqa, h = hk * p.gqa + qr % p.gqa;
+        float *mp = p.part_ml + (part_base(p, s, hk, qr, t, h) + split) * 2;
+        *(float2 *) mp = make_float2(m_run, l);
     }
 }
 
-template <int D, int NRT>
+template <int D, int NW>
 static hipError_t launch_q8_t(const AttnParams &p, hipStream_t stream) {
-    hipLaunchKernelGGL((pa_decode_q8_kernel<D, NRT>), dim3(p.max_splits, p.Hkv, p.S), dim3(64), 0, stream, p);
+    const int64_t npair = (int64_t) p.max_splits * p.S;
+    const int64_t nwg = 8 * (int64_t) p.Hkv * ((npair + 7) / 8);
+    if (nwg > INT32_MAX) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((pa_decode_q8_kernel<D, NW>), dim3((unsigned) nwg), dim3(64 * NW), 0, stream, p);
     const hipError_t e = hipGetLastError();
     return e != hipSuccess ? e : launch_merge(p, D, stream);
 }
 
 hipError_t launch_decode_q8(const AttnParams &p, int head_dim, hipStream_t stream) {
-    const int nrt = p.decode_rows > 16 ? 2 : 1;
+    const int nw = p.decode_rows > 16 ? 2 : 1;
     switch (head_dim) {
-        case 64: return nrt == 1 ? launch_q8_t<64, 1>(p, stream) : launch_q8_t<64, 2>(p, stream);
-        case 128: return nrt == 1 ? launch_q8_t<128, 1>(p, stream) : launch_q8_t<128, 2>(p, stream);
-        case 256: return nrt == 1 ? launch_q8_t<256, 1>(p, stream) : launch_q8_t<256, 2>(p, stream);
+        case 64: return nw == 1 ? launch_q8_t<64, 1>(p, stream) : launch_q8_t<64, 2>(p, stream);
+        case 128: return nw == 1 ? launch_q8_t<128, 1>(p, stream) : launch_q8_t<128, 2>(p, stream);
+        case 256: return nw == 1 ? launch_q8_t<256, 1>(p, stream) : launch_q8_t<256, 2>(p, stream);
         default: return hipErrorInvalidValue;
     }
 }

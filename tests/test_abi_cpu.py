@@ -62,6 +62,11 @@ def test_workspace_size(lib):
     assert workspace_size(-1, 64, 32, 8, 128, 512, 16) == 0
     assert workspace_size(64, 64, 32, 0, 128, 512, 16) == 0
     assert workspace_size(0, 0, 32, 8, 128, 512, 16) > 0
+    # prefill-heavy batch: partials live in (seq, kv head, decode row) slots, so
+    # the workspace stops growing with the token count
+    big = workspace_size(2080, 36, 32, 8, 128, 290, 16)
+    assert big == workspace_size(8000, 36, 32, 8, 128, 290, 16)
+    assert big < workspace_size(2080, 2080, 32, 8, 128, 290, 16)
 
 
 def call_attention(lib, **over):

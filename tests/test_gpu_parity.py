@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import F16, F32, Q8_0, make_case, row_rel_err
+from helpers import F16, F32, Q8_0, decode_rows_f64, make_case, row_rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -141,6 +141,9 @@ SMALL = {
     "q8_long_splits": (8, 2, 128, [9000, 5000], [1, 1], {"k_type": Q8_0}),
     "q8_block_size_32": (8, 2, 128, [500, 61], [1, 4], {"k_type": Q8_0, "bs": 32}),
     "q8_softcap": (8, 2, 128, [333, 77], [1, 3], {"k_type": Q8_0, "softcap": 30.0}),
+    # spec-verify launch (rows per kv head up to 32) holding sequences of 4 and 8 rows too
+    "mixed_rows": (32, 8, 128, [600, 90, 1500], [1, 5, 2], {}),
+    "q8_mixed_rows": (32, 8, 128, [600, 90, 1500], [1, 5, 2], {"k_type": Q8_0}),
 }
 
 
@@ -158,6 +161,31 @@ def test_attention_small_cases(pa, oracle, name):
     assert int(err.item()) == 0
     assert np.isfinite(got).all()
     assert e.max() <= TOL, (name, e.max())
+
+
+@pytest.mark.parametrize("k_type,nq", [(F16, 1), (F16, 5), (Q8_0, 1), (Q8_0, 5)])
+def test_attention_growing_scores(pa, oracle, k_type, nq):
+    """K rows scaled by a ramp 1 .. 16 along each sequence, so every row's
+    running max keeps rising by many log2 units: exercises the online-softmax
+    rescale of O and l on most tiles (random N(0,1) data barely moves the max
+    after the first tile)."""
+    banner(f"growing scores k_type={k_type} nq={nq}")
+    rng = np.random.default_rng(46 + nq + k_type)
+    c = make_case(rng, 32, 8, 128, [1300, 2100, 90], [nq] * 3, k_type=k_type, quantize=oracle.quantize_q8_0)
+    n_embd = c.Hkv * c.D
+    rows = decode_rows_f64(c.k_pool, c.k_type, n_embd).astype(np.float32)
+    for s in range(len(c.seq_lens)):
+        L = int(c.seq_lens[s])
+        i = np.arange(L)
+        cells = c.bt[s, i // c.bs].astype(np.int64) * c.bs + i % c.bs
+        rows[cells] *= (1.0 + 15.0 * i / max(L - 1, 1))[:, None].astype(np.float32)
+    c.k_pool = (oracle.f32_to_f16_bits(rows).view(np.uint8).reshape(rows.shape[0], -1) if k_type == F16
+                else oracle.quantize_q8_0(rows))
+    got = gpu_attention(pa, c)
+    e = row_rel_err(got, oracle_attention(oracle, c))
+    print(f"[gpu] growing scores k_type={k_type} nq={nq}: max row rel err {e.max():.3e}", flush=True)
+    assert np.isfinite(got).all()
+    assert e.max() <= TOL, e.max()
 
 
 def test_attention_all_masked_rows_are_zero(pa, oracle):
