@@ -43,7 +43,7 @@ __device__ __forceinline__ f16x8 lds_tr_b16x8(const char *p0, const char *p1) {
 }
 
 template <int D, int NRT, int NW>
-__global__ __launch_bounds__(NW * 64) void pa_prefill_f16_kernel(AttnParams p, int n_rb) {
+__global__ __launch_bounds__(NW * 64, (D <= 128) ? 2 : 1) void pa_prefill_f16_kernel(AttnParams p, int n_rb) {
     using SH = PrefillShape<D>;
     constexpr int KS = SH::KS, NPV = SH::NPV, STRIDE = SH::STRIDE;
     constexpr int CPT = SH::CHUNKS / (NW * 64);   // 16-byte chunks per thread per tensor
@@ -196,35 +196,42 @@ __global__ __launch_bounds__(NW * 64) void pa_prefill_f16_kernel(AttnParams p, i
                 for (int e = 0; e < 8; e++)
                     if (cell_masked(tile + 8 * g + e, L, prow[rt], p.causal, p.n_swa)) sv[e] = -INFINITY;
             }
-            float mt = sv[0];
+            // Lazy rescale: the row's reference max m_run moves only when a
+            // score exceeds it by more than kRescaleSlack; the test is on the
+            // lane's own 8 cells, and the row-wide max is formed only on the
+            // (rare, wave-uniform) tiles where some lane trips it.
+            float lmax = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
+                               fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+            if (__builtin_amdgcn_ballot_w64(lmax > m_run[rt] + kRescaleSlack)) {
+                const float mt = wave_max(lmax);
+                const bool grow = mt > m_run[rt] + kRescaleSlack;
+                const float mnew = grow ? mt : m_run[rt];
+                const float alpha = grow ? __builtin_amdgcn_exp2f(m_run[rt] - mnew) : 1.f;   // 0 from -inf
+                m_run[rt] = mnew;
+                l_run[rt] *= alpha;
 #pragma unroll
-            for (int e = 1; e < 8; e++) mt = fmaxf(mt, sv[e]);
-            mt = wave_max(mt);
-            const float mnew = fmaxf(m_run[rt], mt);
-            float alpha = 1.f;
-            float pv[8];
-            if (mnew == -INFINITY) {
+                for (int i = 0; i < 4; i++) {
+                    const float a = __shfl(alpha, 4 * g + i);   // alpha of O row 4g+i
 #pragma unroll
-                for (int e = 0; e < 8; e++) pv[e] = 0.f;
-            } else {
-                alpha = __builtin_amdgcn_exp2f(m_run[rt] - mnew);
-#pragma unroll
-                for (int e = 0; e < 8; e++) pv[e] = __builtin_amdgcn_exp2f(sv[e] - mnew);
+                    for (int m = 0; m < NPV; m++) o[rt][m][i] *= a;
+                }
             }
-            m_run[rt] = mnew;
-            float ps = 0.f;
-#pragma unroll
-            for (int e = 0; e < 8; e++) ps += pv[e];
-            l_run[rt] = l_run[rt] * alpha + ps;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float a = __shfl(alpha, 4 * g + i);
-#pragma unroll
-                for (int m = 0; m < NPV; m++) o[rt][m][i] *= a;
-            }
+            // a row with m_run = -inf has only masked cells so far: its P is 0
+            const float mref = m_run[rt] == -INFINITY ? 0.f : m_run[rt];
+            // The row sum accumulates the f16 P the PV MFMA consumes (lane-partial;
+            // reduced over the lane groups at the end).  Each f16 pair is its own
+            // value: hipcc (ROCm 7.2) fed v_dot2c the first dword four times when
+            // the pairs were taken as elements of the packed u32x4.
+            typedef _Float16 f16x2v __attribute__((ext_vector_type(2)));
+            const f16x2v one2 = {(_Float16) 1.0f, (_Float16) 1.0f};
             u32x4 pk;
 #pragma unroll
-            for (int wi = 0; wi < 4; wi++) pk[wi] = pack_f16x2(pv[2 * wi], pv[2 * wi + 1]);
+            for (int wi = 0; wi < 4; wi++) {
+                const f16x2v h2 = {(_Float16) __builtin_amdgcn_exp2f(sv[2 * wi] - mref),
+                                   (_Float16) __builtin_amdgcn_exp2f(sv[2 * wi + 1] - mref)};
+                l_run[rt] = __builtin_amdgcn_fdot2(h2, one2, l_run[rt], false);
+                pk[wi] = __builtin_bit_cast(uint32_t, h2);
+            }
             pa[rt] = __builtin_bit_cast(f16x8, pk);
         }
         const char *vrow = Vl + (8 * g + (n >> 2)) * STRIDE + 8 * (n & 3);
