@@ -138,14 +138,20 @@ __global__ __launch_bounds__(NW * 64, (D <= 128) ? 2 : 1) void pa_prefill_f16_ke
 
     const int bs_mask = (1 << p.bs_log2) - 1;
     const int64_t head_off = (int64_t) hk * D * 2;
+    // block-table entries of 64 logical blocks, one per lane, handed out with
+    // lane shuffles: a tile's loads never wait on a table read
+    TableWindow tw;
+    if (c_lo < c_hi) table_load(p, s, c_lo >> p.bs_log2, L, tw);
     u32x4 kst[CPT], vst[CPT];
     auto load_global = [&](int tile) {
+        if (((min(tile + kTile - 1, L - 1) >> p.bs_log2) - tw.first) >= 64) table_load(p, s, tile >> p.bs_log2, L, tw);
 #pragma unroll
         for (int j = 0; j < CPT; j++) {
             const int q = tid + j * NW * 64;
             const int cell = q / (D / 8), col = q % (D / 8);
             const int c = min(tile + cell, L - 1);
-            const int64_t row = ((int64_t) phys_block(p, s, c >> p.bs_log2) << p.bs_log2) | (c & bs_mask);
+            const int32_t blk = __shfl(tw.id, (c >> p.bs_log2) - tw.first);
+            const int64_t row = ((int64_t) blk << p.bs_log2) | (c & bs_mask);
             kst[j] = *(const u32x4 *) (p.k_pool + row * p.k_row + head_off + col * 16);
             vst[j] = *(const u32x4 *) (p.v_pool + row * p.v_row + head_off + col * 16);
         }
