@@ -74,6 +74,33 @@ WorkspaceLayout workspace_layout(int32_t n_tokens, int32_t n_seqs, int32_t n_hea
     return l;
 }
 
+// Side stream and fork/join events of one host thread for one device, created
+// on first use (default priority, non-blocking) and kept for the life of the
+// process.  Per thread, so concurrent callers never share an event.
+struct SideStream {
+    hipStream_t stream = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
+};
+
+constexpr int kMaxDevices = 64;
+
+const SideStream *side_stream_for(hipStream_t caller) {
+    int dev = 0;
+    if (hipStreamGetDevice(caller, &dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+    thread_local SideStream slots[kMaxDevices];
+    SideStream &s = slots[dev];
+    if (s.join) return &s;
+    int cur = 0;
+    if (hipGetDevice(&cur) != hipSuccess) return nullptr;
+    if (cur != dev && hipSetDevice(dev) != hipSuccess) return nullptr;
+    bool ok = (s.stream || hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking) == hipSuccess) &&
+              (s.fork || hipEventCreateWithFlags(&s.fork, hipEventDisableTiming) == hipSuccess) &&
+              hipEventCreateWithFlags(&s.join, hipEventDisableTiming) == hipSuccess;
+    if (!ok) s.join = nullptr;
+    if (cur != dev && hipSetDevice(cur) != hipSuccess) ok = false;
+    return ok ? &s : nullptr;
+}
+
 int log2_exact(int32_t v) {
     if (v <= 0 || (v & (v - 1))) return -1;
     int l = 0;
@@ -208,13 +235,23 @@ int iian_pa_attention(void *stream, const float *q, const void *k_pool, const vo
     // Q8_0 pools have the decode / spec-verify kernel only (up to 32 rows per kv head)
     if (type_k == IIAN_PA_TYPE_Q8_0 && max_rows > p.decode_rows) return IIAN_PA_ERR_UNSUPPORTED;
     hipStream_t st = (hipStream_t) stream;
-    hipError_t e = launch_decode(p, head_dim, type_k, st);
-    if (e != hipSuccess) return IIAN_PA_ERR_HIP;
-    if (max_rows > p.decode_rows) {
-        e = launch_prefill(p, head_dim, type_k, max_rows, st);
-        if (e != hipSuccess) return IIAN_PA_ERR_HIP;
-    }
-    return IIAN_PA_OK;
+    if (max_rows <= p.decode_rows)
+        return launch_decode(p, head_dim, type_k, st) == hipSuccess ? IIAN_PA_OK : IIAN_PA_ERR_HIP;
+
+    // Mixed batch: the decode rows (HBM-bound) run on a side stream forked from
+    // and joined back into the caller's stream, beside the MFMA-bound prefill
+    // kernel, which fills the CUs first and leaves its tail to the decode waves.
+    const SideStream *side = side_stream_for(st);
+    if (!side) return IIAN_PA_ERR_HIP;
+    if (hipEventRecord(side->fork, st) != hipSuccess || hipStreamWaitEvent(side->stream, side->fork, 0) != hipSuccess)
+        return IIAN_PA_ERR_HIP;
+    if (launch_prefill(p, head_dim, type_k, max_rows, st) != hipSuccess) return IIAN_PA_ERR_HIP;
+    const hipError_t ed = launch_decode(p, head_dim, type_k, side->stream);
+    // join even when the decode launch failed, so the caller's stream never
+    // runs ahead of work queued on the side stream
+    if (hipEventRecord(side->join, side->stream) != hipSuccess || hipStreamWaitEvent(st, side->join, 0) != hipSuccess)
+        return IIAN_PA_ERR_HIP;
+    return ed == hipSuccess ? IIAN_PA_OK : IIAN_PA_ERR_HIP;
 }
 
 int iian_pa_dequant_q8_0(void *stream, const void *pool, int64_t n_cells, const int64_t *rows_idx, int64_t n_rows,

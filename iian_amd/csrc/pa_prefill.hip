@@ -27,8 +27,14 @@ template <int D>
 struct PrefillShape {
     static constexpr int KS = D / 32;                 // QK^T k-steps
     static constexpr int NPV = D / 16;                // PV MFMAs (16 output dims each)
-    static constexpr int STRIDE = D * 2 + 16;         // padded LDS row (bytes)
-    static constexpr int TILE_BYTES = kTile * STRIDE;
+    // Padded LDS rows, both tiles stored in the order their readers walk the
+    // cells: LDS row 16h + 4j + i holds cell 8j + 4h + i.  The QK^T A operand
+    // (half h) then reads 16 consecutive K rows, each 4 banks after the last,
+    // and a V transpose read (cells 8g + i, then 8g + 4 + i) reads rows 4g + i
+    // (resp. 16 + 4g + i), 32 bytes each, 8 banks apart.
+    static constexpr int KSTRIDE = D * 2 + 16;
+    static constexpr int VSTRIDE = D * 2 + 32;
+    static constexpr int TILE_BYTES = kTile * VSTRIDE;
     static constexpr int CHUNKS = kTile * (D / 8);    // 16-byte chunks per tile per tensor
 };
 
@@ -45,7 +51,7 @@ __device__ __forceinline__ f16x8 lds_tr_b16x8(const char *p0, const char *p1) {
 template <int D, int NRT, int NW>
 __global__ __launch_bounds__(NW * 64, (D <= 128) ? 2 : 1) void pa_prefill_f16_kernel(AttnParams p, int n_rb) {
     using SH = PrefillShape<D>;
-    constexpr int KS = SH::KS, NPV = SH::NPV, STRIDE = SH::STRIDE;
+    constexpr int KS = SH::KS, NPV = SH::NPV, KSTRIDE = SH::KSTRIDE, VSTRIDE = SH::VSTRIDE;
     constexpr int CPT = SH::CHUNKS / (NW * 64);   // 16-byte chunks per thread per tensor
     static_assert(CPT * NW * 64 == SH::CHUNKS, "tile chunks must divide evenly");
     constexpr int ROWS = NW * NRT * 16;
@@ -161,8 +167,9 @@ __global__ __launch_bounds__(NW * 64, (D <= 128) ? 2 : 1) void pa_prefill_f16_ke
         for (int j = 0; j < CPT; j++) {
             const int q = tid + j * NW * 64;
             const int cell = q / (D / 8), col = q % (D / 8);
-            *(u32x4 *) (&lds[buf][0][cell * STRIDE + col * 16]) = kst[j];
-            *(u32x4 *) (&lds[buf][1][cell * STRIDE + col * 16]) = vst[j];
+            const int lrow = ((cell >> 2) & 1) * 16 + (cell >> 3) * 4 + (cell & 3);
+            *(u32x4 *) (&lds[buf][0][lrow * KSTRIDE + col * 16]) = kst[j];
+            *(u32x4 *) (&lds[buf][1][lrow * VSTRIDE + col * 16]) = vst[j];
         }
     };
 
@@ -177,9 +184,10 @@ __global__ __launch_bounds__(NW * 64, (D <= 128) ? 2 : 1) void pa_prefill_f16_ke
         f16x8 ka[2][KS];
 #pragma unroll
         for (int h = 0; h < 2; h++) {
-            const int cr = 8 * (n >> 2) + 4 * h + (n & 3);
+            // A operand row n of half h = cell 8(n/4) + 4h + n%4 = LDS row 16h + n
 #pragma unroll
-            for (int ks = 0; ks < KS; ks++) ka[h][ks] = *(const f16x8 *) (Kl + cr * STRIDE + (32 * ks + 8 * g) * 2);
+            for (int ks = 0; ks < KS; ks++)
+                ka[h][ks] = *(const f16x8 *) (Kl + (16 * h + n) * KSTRIDE + (32 * ks + 8 * g) * 2);
         }
         f16x8 pa[NRT];
 #pragma unroll
@@ -240,10 +248,10 @@ __global__ __launch_bounds__(NW * 64, (D <= 128) ? 2 : 1) void pa_prefill_f16_ke
             }
             pa[rt] = __builtin_bit_cast(f16x8, pk);
         }
-        const char *vrow = Vl + (8 * g + (n >> 2)) * STRIDE + 8 * (n & 3);
+        const char *vrow = Vl + (4 * g + (n >> 2)) * VSTRIDE + 8 * (n & 3);
 #pragma unroll
         for (int m = 0; m < NPV; m++) {
-            const f16x8 vb = lds_tr_b16x8(vrow + 32 * m, vrow + 4 * STRIDE + 32 * m);
+            const f16x8 vb = lds_tr_b16x8(vrow + 32 * m, vrow + 16 * VSTRIDE + 32 * m);
 #pragma unroll
             for (int rt = 0; rt < NRT; rt++) o[rt][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[rt], vb, o[rt][m], 0, 0, 0);
         }
@@ -299,8 +307,8 @@ hipError_t launch_prefill(const AttnParams &p, int head_dim, int kv_type, int ma
     if (kv_type != 1) return hipErrorInvalidValue;
     switch (head_dim) {
         case 64: return launch_prefill_t<64, 2, 4>(p, max_rows, stream);
-        case 128: return launch_prefill_t<128, 2, 4>(p, max_rows, stream);
-        case 256: return launch_prefill_t<256, 2, 4>(p, max_rows, stream);
+        case 128: return launch_prefill_t<128, 1, 8>(p, max_rows, stream);
+        case 256: return launch_prefill_t<256, 1, 8>(p, max_rows, stream);
         default: return hipErrorInvalidValue;
     }
 }

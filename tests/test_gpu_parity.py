@@ -188,6 +188,27 @@ def test_attention_growing_scores(pa, oracle, k_type, nq):
     assert e.max() <= TOL, e.max()
 
 
+def test_mixed_batch_on_a_side_stream_of_the_caller(pa, oracle):
+    """A prefill + decode batch forks its decode rows onto the library's side
+    stream and joins them back: issued on a non-default torch stream, three
+    back-to-back calls into three outputs are all complete once that stream
+    is synchronised."""
+    banner("mixed batch on a caller stream")
+    rng = np.random.default_rng(47)
+    c = make_case(rng, 32, 8, 128, [900, 1500, 700, 3000], [200, 1, 1, 1])
+    k, v, batch = to_device(pa, c)
+    prm = pa.PagedAttnParams(scale=c.scale)
+    qs = [rng.standard_normal(c.q.shape).astype(np.float32) for _ in range(3)]
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        qd = [torch.as_tensor(x).cuda() for x in qs]
+        outs = [pa.build_paged_attn(x, k, v, c.Hkv, prm, batch) for x in qd]
+    s.synchronize()
+    for x, o in zip(qs, outs):
+        c.q = x
+        assert row_rel_err(o.cpu().numpy(), oracle_attention(oracle, c)).max() <= TOL
+
+
 def test_attention_all_masked_rows_are_zero(pa, oracle):
     banner("all-masked rows")
     rng = np.random.default_rng(42)
