@@ -232,8 +232,6 @@ int iian_pa_attention(void *stream, const float *q, const void *k_pool, const vo
     // the prefill kernel.
     const int max_rows = max_query_len * p.gqa;
     p.decode_rows = (max_rows > 16 && max_rows <= kDecodeRowsMax) ? kDecodeRowsMax : 16;
-    // Q8_0 pools have the decode / spec-verify kernel only (up to 32 rows per kv head)
-    if (type_k == IIAN_PA_TYPE_Q8_0 && max_rows > p.decode_rows) return IIAN_PA_ERR_UNSUPPORTED;
     hipStream_t st = (hipStream_t) stream;
     if (max_rows <= p.decode_rows)
         return launch_decode(p, head_dim, type_k, st) == hipSuccess ? IIAN_PA_OK : IIAN_PA_ERR_HIP;

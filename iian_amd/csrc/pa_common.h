@@ -150,6 +150,18 @@ __device__ __forceinline__ int64_t table_row(const AttnParams &p, const TableWin
     return ((int64_t) blk << p.bs_log2) | (c & ((1 << p.bs_log2) - 1));
 }
 
+// Orders this wave's LDS accesses before every wave's accesses after it
+// (lgkmcnt(0), then s_barrier when the workgroup has several waves).  Unlike
+// __syncthreads it does not wait for the global loads in flight, which are the
+// prefetch of later tiles.
+template <int NW>
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0); vmcnt, expcnt not waited
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    if constexpr (NW > 1) __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 __device__ __forceinline__ bool cell_masked(int c, int L, int prow, int causal, int n_swa) {
     return c >= L || (causal && c > prow) || (n_swa > 0 && prow - c >= n_swa);
 }
@@ -157,6 +169,18 @@ __device__ __forceinline__ bool cell_masked(int c, int L, int prow, int causal, 
 __device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
     const _Float16 ha = (_Float16) a, hb = (_Float16) b;
     return (uint32_t) __builtin_bit_cast(uint16_t, ha) | ((uint32_t) __builtin_bit_cast(uint16_t, hb) << 16);
+}
+
+// 4 int8 (ggml Q8_0 quants) -> 4 exact f16 (two packed pairs): bias to
+// unsigned, v_perm each byte under 0x64 (the f16 1024 + u), subtract 1152.
+__device__ __forceinline__ void i8x4_to_f16(uint32_t x, uint32_t &lo, uint32_t &hi) {
+    typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+    const uint32_t u = x ^ 0x80808080u;                                      // q + 128
+    const uint32_t a = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);   // f16 {1024 + u0, 1024 + u1}
+    const uint32_t b = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);   // f16 {1024 + u2, 1024 + u3}
+    const f16x2_t bias = {(_Float16) 1152.0f, (_Float16) 1152.0f};
+    lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2_t, a) - bias);
+    hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2_t, b) - bias);
 }
 
 // 8 floats x*s -> an f16 pair (hi, lo) with hi = f16(x*s), lo = f16(x*s - hi),

@@ -59,16 +59,6 @@ struct Q8Lds {
     __attribute__((aligned(16))) float vs[Q8Shape<D>::NB][kTile];
 };
 
-// 4 int8 -> 4 exact f16 (two packed pairs).
-__device__ __forceinline__ void i8x4_to_f16(uint32_t x, uint32_t &lo, uint32_t &hi) {
-    const uint32_t u = x ^ 0x80808080u;                                      // q + 128
-    const uint32_t a = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);   // f16 {1024 + u0, 1024 + u1}
-    const uint32_t b = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);   // f16 {1024 + u2, 1024 + u3}
-    const f16x2 bias = {(_Float16) 1152.0f, (_Float16) 1152.0f};
-    lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, a) - bias);
-    hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, b) - bias);
-}
-
 // Raw Q8_0 bytes of one tile of one pool: lane l holds blocks [part*NBL,
 // part*NBL + NBL) of cell tile + l/2 (part = l%2), as the aligned dword window
 // that contains them.  The window never leaves the cell's row: it ends at the
@@ -139,18 +129,6 @@ __device__ __forceinline__ f16x8 lds_tr_b16x8_q8(const char *p0, const char *p1)
     typedef short s16x8 __attribute__((ext_vector_type(8)));
     const s16x8 c = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
     return __builtin_bit_cast(f16x8, c);
-}
-
-// Orders this wave's LDS accesses before every wave's accesses after it
-// (lgkmcnt(0), then s_barrier when the workgroup has several waves).  Unlike
-// __syncthreads it does not wait for the global loads in flight, which are the
-// next tile's prefetch.
-template <int NW>
-__device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0); vmcnt, expcnt not waited
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    if constexpr (NW > 1) __builtin_amdgcn_s_barrier();
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
 template <int D, int NW>

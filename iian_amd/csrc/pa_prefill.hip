@@ -48,14 +48,24 @@ __device__ __forceinline__ f16x8 lds_tr_b16x8(const char *p0, const char *p1) {
     return __builtin_bit_cast(f16x8, c);
 }
 
-template <int D, int NRT, int NW>
-__global__ __launch_bounds__(NW * 64, (D <= 128) ? 2 : 1) void pa_prefill_f16_kernel(AttnParams p, int n_rb) {
+// KVT: pool type, 1 = f16, 8 = ggml Q8_0 (ggml-common.h:251-256).  A Q8_0 tile
+// is staged with one thread per (tensor, cell, block): K as its exact int8
+// values in f16 plus the block scales d as f32 in LDS, applied per cell after
+// each QK^T k-step MFMA (k-step = block), so q*d enters the scores exactly;
+// V as f16(q*d), the correctly rounded dequantised value.
+template <int D, int NRT, int NW, int KVT>
+__global__ __launch_bounds__(NW * 64, (D <= 128) ? 2 : 1) void pa_prefill_kernel(AttnParams p, int n_rb) {
     using SH = PrefillShape<D>;
     constexpr int KS = SH::KS, NPV = SH::NPV, KSTRIDE = SH::KSTRIDE, VSTRIDE = SH::VSTRIDE;
-    constexpr int CPT = SH::CHUNKS / (NW * 64);   // 16-byte chunks per thread per tensor
-    static_assert(CPT * NW * 64 == SH::CHUNKS, "tile chunks must divide evenly");
+    constexpr bool Q8 = KVT == 8;
+    constexpr int CPT = SH::CHUNKS / (NW * 64);   // f16: 16-byte chunks per thread per tensor
+    static_assert(Q8 || CPT * NW * 64 == SH::CHUNKS, "tile chunks must divide evenly");
+    constexpr int NB = D / 32;                    // Q8_0 blocks per head slice
+    constexpr int ITEMS = 2 * kTile * NB;         // Q8_0: (tensor, cell, block) staging items
+    static_assert(!Q8 || ITEMS <= NW * 64, "one Q8_0 staging item per thread");
     constexpr int ROWS = NW * NRT * 16;
     __shared__ __attribute__((aligned(16))) char lds[2][2][SH::TILE_BYTES];
+    __shared__ __attribute__((aligned(16))) float ksc[2][Q8 ? NB : 1][kTile];   // Q8_0 K scales [block][cell]
 
     // XCD-aware mapping: workgroups are dispatched round-robin over the 8 XCDs
     // (bid % 8).  (sequence, kv head) pairs are dealt round-robin to XCDs and
@@ -148,28 +158,73 @@ __global__ __launch_bounds__(NW * 64, (D <= 128) ? 2 : 1) void pa_prefill_f16_ke
     // lane shuffles: a tile's loads never wait on a table read
     TableWindow tw;
     if (c_lo < c_hi) table_load(p, s, c_lo >> p.bs_log2, L, tw);
-    u32x4 kst[CPT], vst[CPT];
+    u32x4 kst[Q8 ? 1 : CPT], vst[Q8 ? 1 : CPT];
+    // Q8_0 item of this thread: tensor (0 = K), cell and block; its 34 bytes
+    // sit 2 bytes into (odd block) or at the start of (even block) an aligned
+    // 9-dword window that stays inside the head slice
+    const int qi_t = tid / (kTile * NB), qi_cell = (tid % (kTile * NB)) / NB, qi_b = tid % NB;
+    const bool qi_live = Q8 && tid < ITEMS;
+    uint32_t qraw[9];
     auto load_global = [&](int tile) {
         if (((min(tile + kTile - 1, L - 1) >> p.bs_log2) - tw.first) >= 64) table_load(p, s, tile >> p.bs_log2, L, tw);
-#pragma unroll
-        for (int j = 0; j < CPT; j++) {
-            const int q = tid + j * NW * 64;
-            const int cell = q / (D / 8), col = q % (D / 8);
-            const int c = min(tile + cell, L - 1);
+        if constexpr (Q8) {
+            const int c = min(tile + qi_cell, L - 1);
             const int32_t blk = __shfl(tw.id, (c >> p.bs_log2) - tw.first);
             const int64_t row = ((int64_t) blk << p.bs_log2) | (c & bs_mask);
-            kst[j] = *(const u32x4 *) (p.k_pool + row * p.k_row + head_off + col * 16);
-            vst[j] = *(const u32x4 *) (p.v_pool + row * p.v_row + head_off + col * 16);
+            if (qi_live) {
+                const int start = hk * NB * 34 + 34 * qi_b;
+                const uint32_t *src = (const uint32_t *) ((qi_t ? p.v_pool + row * p.v_row : p.k_pool + row * p.k_row) +
+                                                          (start & ~3));
+#pragma unroll
+                for (int i = 0; i < 9; i++) qraw[i] = src[i];
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < CPT; j++) {
+                const int q = tid + j * NW * 64;
+                const int cell = q / (D / 8), col = q % (D / 8);
+                const int c = min(tile + cell, L - 1);
+                const int32_t blk = __shfl(tw.id, (c >> p.bs_log2) - tw.first);
+                const int64_t row = ((int64_t) blk << p.bs_log2) | (c & bs_mask);
+                kst[j] = *(const u32x4 *) (p.k_pool + row * p.k_row + head_off + col * 16);
+                vst[j] = *(const u32x4 *) (p.v_pool + row * p.v_row + head_off + col * 16);
+            }
         }
     };
     auto store_lds = [&](int buf) {
+        if constexpr (Q8) {
+            if (!qi_live) return;
+            const int lrow = ((qi_cell >> 2) & 1) * 16 + (qi_cell >> 3) * 4 + (qi_cell & 3);
+            const bool odd = qi_b & 1;   // block starts 2 bytes into the window
+            const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t) (odd ? qraw[0] >> 16 : qraw[0]));
+            typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+            const f16x2_t d2 = {d, d};
+            u32x4 h[4];
 #pragma unroll
-        for (int j = 0; j < CPT; j++) {
-            const int q = tid + j * NW * 64;
-            const int cell = q / (D / 8), col = q % (D / 8);
-            const int lrow = ((cell >> 2) & 1) * 16 + (cell >> 3) * 4 + (cell & 3);
-            *(u32x4 *) (&lds[buf][0][lrow * KSTRIDE + col * 16]) = kst[j];
-            *(u32x4 *) (&lds[buf][1][lrow * VSTRIDE + col * 16]) = vst[j];
+            for (int k = 0; k < 8; k++) {
+                const uint32_t q4 = odd ? qraw[k + 1] : __builtin_amdgcn_alignbyte(qraw[k + 1], qraw[k], 2);
+                uint32_t lo, hi;
+                i8x4_to_f16(q4, lo, hi);
+                if (qi_t) {   // V: f16(q*d)
+                    lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2_t, lo) * d2);
+                    hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2_t, hi) * d2);
+                }
+                h[k >> 1][2 * (k & 1)] = lo;
+                h[k >> 1][2 * (k & 1) + 1] = hi;
+            }
+            char *dst = qi_t ? &lds[buf][1][lrow * VSTRIDE + qi_b * 64] : &lds[buf][0][lrow * KSTRIDE + qi_b * 64];
+#pragma unroll
+            for (int k = 0; k < 4; k++) *(u32x4 *) (dst + 16 * k) = h[k];
+            if (!qi_t) ksc[buf][qi_b][qi_cell] = (float) d;
+        } else {
+#pragma unroll
+            for (int j = 0; j < CPT; j++) {
+                const int q = tid + j * NW * 64;
+                const int cell = q / (D / 8), col = q % (D / 8);
+                const int lrow = ((cell >> 2) & 1) * 16 + (cell >> 3) * 4 + (cell & 3);
+                *(u32x4 *) (&lds[buf][0][lrow * KSTRIDE + col * 16]) = kst[j];
+                *(u32x4 *) (&lds[buf][1][lrow * VSTRIDE + col * 16]) = vst[j];
+            }
         }
     };
 
@@ -197,7 +252,18 @@ __global__ __launch_bounds__(NW * 64, (D <= 128) ? 2 : 1) void pa_prefill_f16_ke
             for (int h = 0; h < 2; h++) {
                 f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int ks = 0; ks < KS; ks++) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[h][ks], qv[rt][ks], acc, 0, 0, 0);
+                for (int ks = 0; ks < KS; ks++) {
+                    if constexpr (Q8) {
+                        // this lane's S^T rows are cells 8g + 4h + i; k-step ks = Q8_0 block ks
+                        const f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[h][ks], qv[rt][ks],
+                                                                               f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                        const f32x4 dk = *(const f32x4 *) &ksc[buf][ks][8 * g + 4 * h];
+#pragma unroll
+                        for (int i = 0; i < 4; i++) acc[i] = fmaf(c[i], dk[i], acc[i]);
+                    } else {
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[h][ks], qv[rt][ks], acc, 0, 0, 0);
+                    }
+                }
 #pragma unroll
                 for (int i = 0; i < 4; i++) sv[4 * h + i] = acc[i];
             }
@@ -293,22 +359,30 @@ __global__ __launch_bounds__(NW * 64, (D <= 128) ? 2 : 1) void pa_prefill_f16_ke
     }
 }
 
-template <int D, int NRT, int NW>
+template <int D, int NRT, int NW, int KVT>
 static hipError_t launch_prefill_t(const AttnParams &p, int max_rows, hipStream_t stream) {
     constexpr int ROWS = NW * NRT * 16;
     const int n_rb = (max_rows + ROWS - 1) / ROWS;
     const int pairs_per_xcd = (p.S * p.Hkv + 7) / 8;
     const int nwg = 8 * pairs_per_xcd * n_rb;
-    hipLaunchKernelGGL((pa_prefill_f16_kernel<D, NRT, NW>), dim3(nwg), dim3(NW * 64), 0, stream, p, n_rb);
+    hipLaunchKernelGGL((pa_prefill_kernel<D, NRT, NW, KVT>), dim3(nwg), dim3(NW * 64), 0, stream, p, n_rb);
     return hipGetLastError();
 }
 
-hipError_t launch_prefill(const AttnParams &p, int head_dim, int kv_type, int max_rows, hipStream_t stream) {
-    if (kv_type != 1) return hipErrorInvalidValue;
+template <int KVT>
+static hipError_t launch_prefill_kv(const AttnParams &p, int head_dim, int max_rows, hipStream_t stream) {
     switch (head_dim) {
-        case 64: return launch_prefill_t<64, 2, 4>(p, max_rows, stream);
-        case 128: return launch_prefill_t<128, 1, 8>(p, max_rows, stream);
-        case 256: return launch_prefill_t<256, 1, 8>(p, max_rows, stream);
+        case 64: return launch_prefill_t<64, 2, 4, KVT>(p, max_rows, stream);
+        case 128: return launch_prefill_t<128, 1, 8, KVT>(p, max_rows, stream);
+        case 256: return launch_prefill_t<256, 1, 8, KVT>(p, max_rows, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_prefill(const AttnParams &p, int head_dim, int kv_type, int max_rows, hipStream_t stream) {
+    switch (kv_type) {
+        case 1: return launch_prefill_kv<1>(p, head_dim, max_rows, stream);
+        case 8: return launch_prefill_kv<8>(p, head_dim, max_rows, stream);
         default: return hipErrorInvalidValue;
     }
 }

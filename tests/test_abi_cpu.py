@@ -86,7 +86,6 @@ def call_attention(lib, **over):
     ({"q": None}, -1), ({"k": None}, -1), ({"bt": None}, -1), ({"out": None}, -1), ({"pos": None}, -1),
     ({"H": 6, "Hkv": 4}, -2), ({"Hkv": 0}, -2), ({"T": -1}, -2), ({"maxq": 5}, -2), ({"num_blocks": 0}, -2),
     ({"n_swa": -1}, -2), ({"softcap": -1.0}, -2), ({"scale": float("nan")}, -2), ({"q": 0x1004}, -2),
-    ({"tk": 8, "tv": 8, "H": 32, "Hkv": 2, "maxq": 4}, -3),   # Q8_0 pools: no prefill kernel (64 rows)
     ({"tk": 8, "tv": 8, "D": 96, "Dv": 96}, -3), ({"tk": 0, "tv": 0}, -3), ({"tk": 1, "tv": 0}, -3), ({"D": 96, "Dv": 96}, -3),
     ({"bs": 12}, -3), ({"bs": 4}, -3),
     ({"ws": None}, -4), ({"ws_bytes": 16}, -4),

@@ -141,6 +141,13 @@ SMALL = {
     "q8_long_splits": (8, 2, 128, [9000, 5000], [1, 1], {"k_type": Q8_0}),
     "q8_block_size_32": (8, 2, 128, [500, 61], [1, 4], {"k_type": Q8_0, "bs": 32}),
     "q8_softcap": (8, 2, 128, [333, 77], [1, 3], {"k_type": Q8_0, "softcap": 30.0}),
+    # Q8_0 pools through the prefill kernel
+    "q8_prefill_d128": (32, 8, 128, [600, 200], [512, 70], {"k_type": Q8_0}),
+    "q8_prefill_d64": (14, 2, 64, [400], [130], {"k_type": Q8_0}),
+    "q8_prefill_d256": (16, 8, 256, [700, 300], [256, 33], {"k_type": Q8_0}),
+    "q8_mixed_prefill_decode": (32, 8, 128, [900, 1500, 700, 64], [256, 1, 1, 64], {"k_type": Q8_0}),
+    "q8_swa_prefill": (16, 8, 256, [2000, 1200], [256, 100], {"k_type": Q8_0, "n_swa": 512}),
+    "q8_prefill_softcap": (8, 2, 128, [333, 77], [1, 40], {"k_type": Q8_0, "softcap": 30.0}),
     # spec-verify launch (rows per kv head up to 32) holding sequences of 4 and 8 rows too
     "mixed_rows": (32, 8, 128, [600, 90, 1500], [1, 5, 2], {}),
     "q8_mixed_rows": (32, 8, 128, [600, 90, 1500], [1, 5, 2], {"k_type": Q8_0}),
