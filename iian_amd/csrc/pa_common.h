@@ -188,12 +188,21 @@ __device__ __forceinline__ void i8x4_to_f16(uint32_t x, uint32_t &lo, uint32_t &
 // relative error, and a score error of |s|*2^-11 becomes visible once the
 // softmax is peaked (|s| of tens); the extra MFMA per k-step over lo keeps the
 // scores at the reference's f32 q precision.
+//
+// hi and the difference pass through empty asm so that the compiler cannot
+// fold "x*s - hi" into a v_fma_mix*_f16 with a negated operand: on MI355X
+// (ROCm 7.2 hipcc) that form came out as hi - x*s, i.e. hi + lo = 2hi - x,
+// twice the error of a plain f16 q (found by the peaked-softmax parity tests).
 __device__ __forceinline__ void split_f16x8(const float4 &a, const float4 &b, float s, f16x8 &hi, f16x8 &lo) {
     const float x[8] = {a.x * s, a.y * s, a.z * s, a.w * s, b.x * s, b.y * s, b.z * s, b.w * s};
 #pragma unroll
     for (int e = 0; e < 8; e++) {
-        hi[e] = (_Float16) x[e];
-        lo[e] = (_Float16) (x[e] - (float) hi[e]);
+        float h = (float) (_Float16) x[e];
+        asm volatile("" : "+v"(h));
+        float d = x[e] - h;
+        asm volatile("" : "+v"(d));
+        hi[e] = (_Float16) h;
+        lo[e] = (_Float16) d;
     }
 }
 

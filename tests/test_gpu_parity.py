@@ -170,12 +170,14 @@ def test_attention_small_cases(pa, oracle, name):
     assert e.max() <= TOL, (name, e.max())
 
 
-@pytest.mark.parametrize("k_type,nq", [(F16, 1), (F16, 5), (Q8_0, 1), (Q8_0, 5)])
+@pytest.mark.parametrize("k_type,nq", [(F16, 1), (F16, 5), (F16, 64), (Q8_0, 1), (Q8_0, 5), (Q8_0, 64)])
 def test_attention_growing_scores(pa, oracle, k_type, nq):
     """K rows scaled by a ramp 1 .. 16 along each sequence, so every row's
     running max keeps rising by many log2 units: exercises the online-softmax
     rescale of O and l on most tiles (random N(0,1) data barely moves the max
-    after the first tile)."""
+    after the first tile), and peaked softmax rows whose scores a single f16 q
+    would get wrong by more than the tolerance.  nq = 1, 5: decode and
+    spec-verify kernels; nq = 64: prefill kernel."""
     banner(f"growing scores k_type={k_type} nq={nq}")
     rng = np.random.default_rng(46 + nq + k_type)
     c = make_case(rng, 32, 8, 128, [1300, 2100, 90], [nq] * 3, k_type=k_type, quantize=oracle.quantize_q8_0)
