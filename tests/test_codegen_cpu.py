@@ -1,0 +1,44 @@
+"""Instruction-selection guards on the gfx950 device code (CPU: hipcc -S only).
+
+Two instruction forms have given wrong results on the MI355X boxes this
+library runs on, silently:
+  * packed FP32 VALU ops (v_pk_add/mul/fma_f32): the build disables them
+    (-packed-fp32-ops); this checks that the flag took effect;
+  * a mixed-precision FMA (v_fma_mix*/v_mad_mix*) with a negated operand: the
+    hi/lo split of q (pa_common.h split_f16x8) was compiled to one and came out
+    as hi - x instead of x - hi (caught by the peaked-score parity tests); the
+    source keeps the compiler from forming it.
+"""
+import re
+import shutil
+import subprocess
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+import pytest
+
+from iian_amd import build as B
+
+KERNEL_SOURCES = ["pa_decode.hip", "pa_decode_q8.hip", "pa_prefill.hip", "pa_kv_write.hip"]
+PACKED_F32 = re.compile(r"^\s*v_pk_(add|mul|fma)_f32\b", re.M)
+NEG_MIX = re.compile(r"^\s*v_(fma|mad)_mix\w*\s[^\n]*,\s*-", re.M)
+
+
+def device_asm(src: str, tmp: Path) -> str:
+    out = tmp / (Path(src).stem + ".s")
+    cmd = [B.hipcc(), *B.HIPCC_FLAGS, "--cuda-device-only", "-S", str(B.CSRC / src), "-o", str(out)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    assert res.returncode == 0, res.stderr[-2000:]
+    return out.read_text()
+
+
+@pytest.mark.skipif(shutil.which("hipcc") is None and not Path("/opt/rocm/bin/hipcc").exists(),
+                    reason="hipcc not available")
+def test_no_packed_fp32_and_no_negated_mixed_fma(tmp_path):
+    with ThreadPoolExecutor(len(KERNEL_SOURCES)) as ex:
+        asms = dict(zip(KERNEL_SOURCES, ex.map(lambda s: device_asm(s, tmp_path), KERNEL_SOURCES)))
+    for src, asm in asms.items():
+        assert "v_mfma" in asm or src == "pa_kv_write.hip", src   # the asm is the kernels'
+        assert not PACKED_F32.search(asm), (src, PACKED_F32.search(asm).group(0))
+        m = NEG_MIX.search(asm)
+        assert m is None, (src, m.group(0) if m else None)
