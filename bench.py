@@ -192,8 +192,9 @@ def main() -> int:
         "attn_tok_per_s": round(w.T / (attn_ms * 1e-3), 1),
         "roofline": {
             "bound": "mfma" if mfma_bound else "hbm",
-            "kernel": "iian_pa_attention (" + ("pa_prefill_f16_kernel" if mfma_bound else
-                                               "pa_decode_f16_kernel + pa_merge_kernel") + ")",
+            "kernel": "iian_pa_attention (" + ("pa_prefill_kernel" if mfma_bound else
+                                               ("pa_decode_q8_kernel" if sp.kv_type == pa.GGML_TYPE_Q8_0
+                                                else "pa_decode_f16_kernel") + " + pa_merge_kernel") + ")",
             "achieved": round(attn_tfs if mfma_bound else attn_gbs, 1),
             "peak": MFMA_F16_PEAK_TFLOPS if mfma_bound else HBM_PEAK_GBS,
             "unit": "TFLOP/s" if mfma_bound else "GB/s",
