@@ -39,10 +39,15 @@ int max_splits_for(int32_t max_blocks, int32_t block_size) {
     return (int) (std::max<int64_t>(ns, 1) | 1);
 }
 
-int split_cells_for(int64_t n_seqs, int32_t n_head_kv, int64_t window_cells) {
+// Spec-verify calls (up to 32 query rows per kv head) write 2x the partial
+// bytes per split, so their splits may grow to 1024 cells (measured: -3% at
+// config 4; 2048 cells, too few waves, +2%).
+constexpr int kSplitCellsMaxMultiRow = 1024;
+
+int split_cells_for(int64_t n_seqs, int32_t n_head_kv, int64_t window_cells, int max_cells) {
     const int64_t want = n_seqs * n_head_kv * window_cells / kSplitTargetWaves;
     int sc = kSplitCellsMin;
-    while (sc < kSplitCellsMax && 2 * sc <= want) sc *= 2;
+    while (sc < max_cells && 2 * sc <= want) sc *= 2;
     return sc;
 }
 
@@ -217,21 +222,22 @@ int iian_pa_attention(void *stream, const float *q, const void *k_pool, const vo
     p.qscale = softcap > 0.0f ? scale : scale * kLog2e;
     p.causal = causal ? 1 : 0;
     p.n_swa = n_swa;
-    p.max_splits = max_splits_for(max_blocks, block_size);
-    int64_t window = (int64_t) max_blocks * block_size;
-    if (n_swa > 0) window = std::min<int64_t>(window, (int64_t) n_swa + max_query_len + kTile);
-    p.split_cells = split_cells_for(n_seqs, n_head_kv, window);
-    const WorkspaceLayout wl = workspace_layout(n_tokens, n_seqs, n_head, n_head_kv, head_dim_v, p.max_splits);
-    char *ws = (char *) (((uintptr_t) workspace + 255) & ~(uintptr_t) 255);
-    p.part_ml = (float *) (ws + wl.ml);
-    p.part_o = (float *) (ws + wl.o);
-    p.part_by_seq = wl.by_seq ? 1 : 0;
-
     // Row budget of the decode kernel: one 16-row MFMA tile, or two when that
     // covers every sequence of the call (spec-verify); larger sequences go to
     // the prefill kernel.
     const int max_rows = max_query_len * p.gqa;
     p.decode_rows = (max_rows > 16 && max_rows <= kDecodeRowsMax) ? kDecodeRowsMax : 16;
+
+    p.max_splits = max_splits_for(max_blocks, block_size);
+    int64_t window = (int64_t) max_blocks * block_size;
+    if (n_swa > 0) window = std::min<int64_t>(window, (int64_t) n_swa + max_query_len + kTile);
+    p.split_cells = split_cells_for(n_seqs, n_head_kv, window,
+                                    p.decode_rows > 16 ? kSplitCellsMaxMultiRow : kSplitCellsMax);
+    const WorkspaceLayout wl = workspace_layout(n_tokens, n_seqs, n_head, n_head_kv, head_dim_v, p.max_splits);
+    char *ws = (char *) (((uintptr_t) workspace + 255) & ~(uintptr_t) 255);
+    p.part_ml = (float *) (ws + wl.ml);
+    p.part_o = (float *) (ws + wl.o);
+    p.part_by_seq = wl.by_seq ? 1 : 0;
     hipStream_t st = (hipStream_t) stream;
     if (max_rows <= p.decode_rows)
         return launch_decode(p, head_dim, type_k, st) == hipSuccess ? IIAN_PA_OK : IIAN_PA_ERR_HIP;

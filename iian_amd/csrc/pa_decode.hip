@@ -306,8 +306,12 @@ __global__ __launch_bounds__(64) void pa_merge_kernel(AttnParams p) {
     if (w.nq <= 0 || M > p.decode_rows || w.nsplit == 1 || r >= M) return;
     const int t = w.q0 + r / p.gqa, h = hk * p.gqa + r % p.gqa;
     const int64_t base = part_base(p, s, hk, r, t, h);
-    float mx = -INFINITY;
-    for (int sp = lane; sp < w.nsplit; sp += 64) mx = fmaxf(mx, p.part_ml[(base + sp) * 2]);
+    const int ns = w.nsplit;
+    // (m, l) of splits lane, lane + 64, ...: the first chunk stays in registers
+    float2 ml0 = make_float2(-INFINITY, 0.f);
+    if (lane < ns) ml0 = *(const float2 *) (p.part_ml + (base + lane) * 2);
+    float mx = ml0.x;
+    for (int sp = lane + 64; sp < ns; sp += 64) mx = fmaxf(mx, p.part_ml[(base + sp) * 2]);
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
     float acc[DL];
@@ -315,19 +319,27 @@ __global__ __launch_bounds__(64) void pa_merge_kernel(AttnParams p) {
     for (int i = 0; i < DL; i++) acc[i] = 0.f;
     float lpart = 0.f;
     if (mx != -INFINITY) {
-        for (int c0 = 0; c0 < w.nsplit; c0 += 64) {
-            const int nc = min(64, w.nsplit - c0);
-            float wl = 0.f;
-            if (lane < nc) {
-                const float2 ml = *(const float2 *) (p.part_ml + (base + c0 + lane) * 2);
-                wl = __builtin_amdgcn_exp2f(ml.x - mx);   // 0 for an empty split
-                lpart += wl * ml.y;
-            }
-            for (int j = 0; j < nc; j++) {
-                const float wgt = __shfl(wl, j);
-                const float *op = p.part_o + (base + c0 + j) * D + lane * DL;
+        for (int c0 = 0; c0 < ns; c0 += 64) {
+            const int nc = min(64, ns - c0);
+            const float2 ml = c0 == 0 ? ml0 : (lane < nc ? *(const float2 *) (p.part_ml + (base + c0 + lane) * 2)
+                                                         : make_float2(-INFINITY, 0.f));
+            const float wl = lane < nc ? __builtin_amdgcn_exp2f(ml.x - mx) : 0.f;   // 0 for an empty split
+            lpart += wl * ml.y;
+            // partial O rows in batches of 8, all loads of a batch issued before use
+            for (int j0 = 0; j0 < nc; j0 += 8) {
+                float v[8][DL];
 #pragma unroll
-                for (int i = 0; i < DL; i++) acc[i] += wgt * op[i];
+                for (int u = 0; u < 8; u++) {
+                    const float *op = p.part_o + (base + c0 + min(j0 + u, nc - 1)) * D + lane * DL;
+#pragma unroll
+                    for (int i = 0; i < DL; i++) v[u][i] = op[i];
+                }
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    const float wgt = j0 + u < nc ? __shfl(wl, min(j0 + u, 63)) : 0.f;
+#pragma unroll
+                    for (int i = 0; i < DL; i++) acc[i] += wgt * v[u][i];
+                }
             }
         }
     }
