@@ -13,69 +13,37 @@ namespace {
 
 using namespace iian_pa;
 
-// Split-K partition of the decode kernels.  A split covers split_cells cells
-// (a power of two in [kSplitCellsMin, kSplitCellsMax]), chosen per call so
-// that the (sequence, kv head, split) waves number about kSplitTargetWaves for
-// the call's largest possible window: long contexts keep 512-cell splits,
-// small batches or short windows are cut finer so each wave's chain of
-// dependent tile loads stays short.
-constexpr int kSplitCellsMax = 512;
-constexpr int kSplitCellsMin = 64;
-constexpr int64_t kSplitTargetWaves = 4096;
-// The workspace always admits at least this many splits per row (when the
-// table has the cells for them), so a fine split is never capped by it.
-constexpr int kMinSplitsCap = 16;
+// Stream-K workers of the decode kernels (for_each_piece, pa_common.h): the
+// f16 kernel runs kDecodeWaves single-wave workgroups, which is every slot of
+// a 256-CU MI355X at its two waves per SIMD, so each wave's equal share of the
+// call runs at once and the kernel ends with no tail.  The Q8_0 kernel's
+// workers are groups of Hkv workgroups of NW waves over the same wave count.
+constexpr int kDecodeWaves = 2048;
 
-// Splits per partial row (also the row stride of the partials, in records).
-// Always odd: with an even count such as 16 the D*4-byte records put every
-// row at a power-of-two stride, which aliases the rows onto the same HBM
-// channels (measured on MI355X: 190 us instead of 151 us at the Llama-3-8B
-// decode shape).
-int max_splits_for(int32_t max_blocks, int32_t block_size) {
-    const int64_t cells = (int64_t) max_blocks * block_size + kTile;
-    const int64_t coarse = (cells + kSplitCellsMax - 1) / kSplitCellsMax;
-    const int64_t fine = (cells + kSplitCellsMin - 1) / kSplitCellsMin;
-    const int64_t ns = std::max(coarse, std::min<int64_t>(fine, kMinSplitsCap));
-    return (int) (std::max<int64_t>(ns, 1) | 1);
-}
+int q8_waves_per_wg(int decode_rows) { return decode_rows > 16 ? 2 : 1; }   // NW of pa_decode_q8_kernel
 
-// Spec-verify calls (up to 32 query rows per kv head) write 2x the partial
-// bytes per split, so their splits may grow to 1024 cells (measured: -3% at
-// config 4; 2048 cells, too few waves, +2%).
-constexpr int kSplitCellsMaxMultiRow = 1024;
+// Workspace: [partial records (numerators)][(m, l) per record row][segment
+// info], each section 256-byte aligned.  Sized for the record count of
+// either kernel at kDecodeRowsMax rows: the f16 kernel has at most
+// kDecodeWaves + S*Hkv one-head records, the Q8_0 kernel at most
+// kDecodeWaves/Hkv + S records of Hkv heads.  A record is padded by 64 floats
+// so that consecutive records do not sit at a power-of-two stride (rows at
+// such strides alias onto the same HBM channels).
+constexpr int kRecordPad = 64;
 
-int split_cells_for(int64_t n_seqs, int32_t n_head_kv, int64_t window_cells, int max_cells) {
-    const int64_t want = n_seqs * n_head_kv * window_cells / kSplitTargetWaves;
-    int sc = kSplitCellsMin;
-    while (sc < max_cells && 2 * sc <= want) sc *= 2;
-    return sc;
-}
-
-// Partial rows: (token, head), or (sequence, kv head, decode row) slots when
-// those are fewer (prefill tokens never use partials).
-int64_t partial_rows(int32_t n_tokens, int32_t n_seqs, int32_t n_head, int32_t n_head_kv, bool &by_seq) {
-    const int64_t by_token = (int64_t) n_tokens * n_head;
-    const int64_t by_slot = (int64_t) n_seqs * n_head_kv * kDecodeRowsMax;
-    by_seq = by_slot < by_token;
-    return by_seq ? by_slot : by_token;
-}
-
-// Workspace: [partial (m, l) rows*splits*2 f32][partial O rows*splits*Dv f32],
-// each section 256-byte aligned.
 struct WorkspaceLayout {
-    size_t ml, o, total;
-    bool by_seq;
+    size_t o, ml, seg, total;
 };
 
 inline size_t align256(size_t v) { return (v + 255) & ~(size_t) 255; }
 
-WorkspaceLayout workspace_layout(int32_t n_tokens, int32_t n_seqs, int32_t n_head, int32_t n_head_kv,
-                                 int32_t head_dim_v, int max_splits) {
+WorkspaceLayout workspace_layout(int32_t n_seqs, int32_t n_head_kv, int32_t head_dim_v) {
+    const size_t rec_heads = (size_t) kDecodeWaves + (size_t) n_seqs * n_head_kv;   // records x heads, upper bound
     WorkspaceLayout l;
-    const size_t rows = (size_t) partial_rows(n_tokens, n_seqs, n_head, n_head_kv, l.by_seq) * max_splits;
-    l.ml = 0;
-    l.o = l.ml + align256(rows * 2 * sizeof(float));
-    l.total = l.o + align256(rows * head_dim_v * sizeof(float));
+    l.o = 0;
+    l.ml = l.o + align256((rec_heads * kDecodeRowsMax * head_dim_v + rec_heads * kRecordPad) * sizeof(float));
+    l.seg = l.ml + align256(rec_heads * kDecodeRowsMax * 2 * sizeof(float));
+    l.total = l.seg + align256((size_t) n_seqs * n_head_kv * sizeof(int2));
     return l;
 }
 
@@ -167,9 +135,7 @@ size_t iian_pa_workspace_size(int32_t n_tokens, int32_t n_seqs, int32_t n_head, 
     if (n_tokens < 0 || n_seqs < 0 || n_head <= 0 || n_head_kv <= 0 || head_dim_v <= 0 || max_blocks < 0 ||
         block_size <= 0)
         return 0;
-    const WorkspaceLayout l = workspace_layout(n_tokens, n_seqs, n_head, n_head_kv, head_dim_v,
-                                               max_splits_for(max_blocks, block_size));
-    return l.total + 256;   // room to align the caller's base to 256 bytes
+    return workspace_layout(n_seqs, n_head_kv, head_dim_v).total + 256;   // room to align the caller's base to 256 bytes
 }
 
 int iian_pa_attention(void *stream, const float *q, const void *k_pool, const void *v_pool, int type_k, int type_v,
@@ -228,16 +194,19 @@ int iian_pa_attention(void *stream, const float *q, const void *k_pool, const vo
     const int max_rows = max_query_len * p.gqa;
     p.decode_rows = (max_rows > 16 && max_rows <= kDecodeRowsMax) ? kDecodeRowsMax : 16;
 
-    p.max_splits = max_splits_for(max_blocks, block_size);
-    int64_t window = (int64_t) max_blocks * block_size;
-    if (n_swa > 0) window = std::min<int64_t>(window, (int64_t) n_swa + max_query_len + kTile);
-    p.split_cells = split_cells_for(n_seqs, n_head_kv, window,
-                                    p.decode_rows > 16 ? kSplitCellsMaxMultiRow : kSplitCellsMax);
-    const WorkspaceLayout wl = workspace_layout(n_tokens, n_seqs, n_head, n_head_kv, head_dim_v, p.max_splits);
+    if (type_k == IIAN_PA_TYPE_Q8_0) {
+        p.rec_heads = n_head_kv;
+        p.sk_workers = std::max(1, kDecodeWaves / (q8_waves_per_wg(p.decode_rows) * n_head_kv));
+    } else {
+        p.rec_heads = 1;
+        p.sk_workers = kDecodeWaves;
+    }
+    p.rec_stride = (int64_t) p.rec_heads * p.decode_rows * head_dim_v + kRecordPad;
+    const WorkspaceLayout wl = workspace_layout(n_seqs, n_head_kv, head_dim_v);
     char *ws = (char *) (((uintptr_t) workspace + 255) & ~(uintptr_t) 255);
-    p.part_ml = (float *) (ws + wl.ml);
     p.part_o = (float *) (ws + wl.o);
-    p.part_by_seq = wl.by_seq ? 1 : 0;
+    p.part_ml = (float *) (ws + wl.ml);
+    p.seg_info = (int2 *) (ws + wl.seg);
     hipStream_t st = (hipStream_t) stream;
     if (max_rows <= p.decode_rows)
         return launch_decode(p, head_dim, type_k, st) == hipSuccess ? IIAN_PA_OK : IIAN_PA_ERR_HIP;

@@ -31,11 +31,13 @@ struct AttnParams {
     const int32_t *qsl;         // [S+1]
     const int32_t *pos;         // [T]
     float *out;                 // [T][H][Dv]
-    float *part_o;              // [rows][max_splits][Dv]   split-K partial numerators
-    float *part_ml;             // [rows][max_splits][2]    (reference max in log2 units, sum)
+    float *part_o;              // stream-K partial records: numerators, rec_stride floats per record
+    float *part_ml;             // (reference max in log2 units, sum) per record row
+    int2 *seg_info;             // per segment: (first record, pieces), written by the segment's first piece
     int32_t *err;               // nullable error word
     int64_t k_row;              // bytes per K pool row
     int64_t v_row;
+    int64_t rec_stride;         // floats per record of part_o
     int32_t max_blocks;
     int32_t num_blocks;
     int32_t T, S, H, Hkv, gqa;
@@ -45,20 +47,10 @@ struct AttnParams {
     float softcap_inv;
     int32_t causal;
     int32_t n_swa;
-    int32_t max_splits;
-    int32_t split_cells;
     int32_t decode_rows;        // sequences with n_q*gqa <= decode_rows use the decode kernel
-    int32_t part_by_seq;        // partial rows are (seq, kv head, row < kDecodeRowsMax), else (token, head)
+    int32_t sk_workers;         // stream-K workers: waves (one kv head each) or groups of Hkv workgroups
+    int32_t rec_heads;          // kv heads per partial record: 1, or Hkv for grouped workers
 };
-
-// First split-K partial record of query row r = j*gqa + g (token t, head h)
-// of sequence s at kv head hk.  Partials are indexed by (token, head) unless
-// the call has more of those than (sequence, kv head, decode row) slots (a
-// batch dominated by prefill tokens, which never use partials).
-__device__ __forceinline__ int64_t part_base(const AttnParams &p, int s, int hk, int r, int t, int h) {
-    const int64_t row = p.part_by_seq ? ((int64_t) s * p.Hkv + hk) * kDecodeRowsMax + r : (int64_t) t * p.H + h;
-    return row * p.max_splits;
-}
 
 __device__ __forceinline__ float wave_max(float v) {
     v = fmaxf(v, __shfl_xor(v, 16));
@@ -82,52 +74,140 @@ __device__ __forceinline__ int32_t phys_block(const AttnParams &p, int s, int b)
     return id;
 }
 
-// Cell window of sequence s that any of its query tokens can attend, and its
-// split-K partition.  Identical in the attention and merge kernels.
+// ---- Stream-K partition of the decode work ----
+//
+// A decode sequence (1 <= n_q and n_q*gqa <= decode_rows query rows) attends
+// the window [c_lo, c_hi) of cells that any of its query positions can see
+// (causal and sliding-window bounds; c_lo a multiple of kTile).  Its window is
+// nt = max(1, ceil((c_hi - c_lo)/kTile)) tiles: an empty window keeps one tile,
+// whose piece writes the zero rows of paged_attn.cpp:132.  Laid end to end in
+// sequence order, the windows form one line of tiles; a segment is a
+// (sequence, kv head) stretch of it when each worker is one wave of one kv head
+// (UNIT = Hkv segments per sequence), or a whole sequence when a worker is a
+// group of Hkv workgroups, one per kv head (UNIT = 1).  Worker w takes line
+// tiles [w*per, (w+1)*per) with per = ceil(total / workers), whatever
+// sequences they fall in, so every worker carries the same work however ragged
+// the contexts are.  The stretch of one worker inside one segment is a piece;
+// a segment with one piece writes its output directly, the others write
+// partial records merged by pa_merge_kernel.  Piece (worker w, segment seg) has
+// record w + seg: along the line either w or seg grows by one from piece to
+// piece, so records are unique and a segment's pieces hold consecutive ones.
+constexpr int kMinPieceTiles = 2;
+
 struct SeqWindow {
     int L, q0, nq;
     int pmin, pmax;
-    int c_lo, c_hi;     // [c_lo, c_hi): c_lo a multiple of kTile
-    int chunk, nsplit;
+    int c_lo, c_hi;   // [c_lo, c_hi): c_lo a multiple of kTile
+    int nt;           // tiles of the window; 0 when s is not a decode sequence
 };
 
-__device__ __forceinline__ void split_plan(int range, int split_cells, int max_splits, int &chunk, int &nsplit) {
-    if (range <= 0) { chunk = kTile; nsplit = 1; return; }
-    chunk = split_cells;
-    nsplit = (range + chunk - 1) / chunk;
-    if (nsplit > max_splits) {
-        chunk = (((range + max_splits - 1) / max_splits) + kTile - 1) & ~(kTile - 1);
-        nsplit = (range + chunk - 1) / chunk;
-    }
-}
-
-// pmin/pmax over the sequence's query positions (wave-cooperative; all lanes get the result).
-__device__ __forceinline__ void seq_window(const AttnParams &p, int s, SeqWindow &w) {
-    const int lane = threadIdx.x & 63;
-    w.L = p.seq_lens[s];
+// Window of sequence s (s >= S, or not a decode sequence: nt = 0).  Called
+// per lane (one sequence each) to count tiles, and with a wave-uniform s
+// (scalar loads) for the sequence of a piece.
+__device__ __forceinline__ SeqWindow seq_window(const AttnParams &p, int s) {
+    SeqWindow w = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (s >= p.S) return w;
+    w.L = max(p.seq_lens[s], 0);
     w.q0 = min(max(p.qsl[s], 0), p.T);
     w.nq = min(max(p.qsl[s + 1], w.q0), p.T) - w.q0;
+    if (w.nq <= 0 || w.nq * p.gqa > p.decode_rows) return w;
     int mn = INT32_MAX, mx = INT32_MIN;
-    for (int i = lane; i < w.nq; i += 64) {
+    for (int i = 0; i < w.nq; i++) {
         const int ps = p.pos[w.q0 + i];
         mn = min(mn, ps);
         mx = max(mx, ps);
     }
-    for (int o = 32; o >= 1; o >>= 1) {
-        mn = min(mn, __shfl_xor(mn, o));
-        mx = max(mx, __shfl_xor(mx, o));
-    }
     w.pmin = mn;
     w.pmax = mx;
     int hi = w.L;
-    if (p.causal) hi = min(hi, w.pmax + 1);
+    if (p.causal) hi = min(hi, max(w.pmax + 1, 0));
     int lo = 0;
     if (p.n_swa > 0) lo = max(0, w.pmin - p.n_swa + 1);
     lo &= ~(kTile - 1);
     if (hi < lo) hi = lo;
     w.c_lo = lo;
     w.c_hi = hi;
-    split_plan(hi - lo, p.split_cells, p.max_splits, w.chunk, w.nsplit);
+    w.nt = max(1, (hi - lo + kTile - 1) / kTile);
+    return w;
+}
+
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+__device__ __forceinline__ int wave_incl_scan(int v) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int u = __shfl_up(v, o);
+        if (lane >= o) v += u;
+    }
+    return v;
+}
+
+// One piece of a worker's range: sequence s (window w), kv head hk, window
+// tiles [t0, t1), partial record rec, and the segment's piece count (1 = the
+// piece is the whole segment and writes the output itself).
+struct Piece {
+    int s, hk, t0, t1, rec, pieces, seg;
+};
+
+// Calls body(w, piece) for each piece of worker `worker` (wave-uniform).
+// GROUPED: one segment per sequence and the worker's kv head is hk_fixed;
+// otherwise segments are (sequence, kv head).
+template <bool GROUPED, typename Body>
+__device__ __forceinline__ void for_each_piece(const AttnParams &p, int worker, int hk_fixed, Body &&body) {
+    const int lane = threadIdx.x & 63;
+    const int unit = GROUPED ? 1 : p.Hkv;
+    // lanes hold the tile counts of sequences base + lane and their inclusive
+    // prefix along the line
+    int nt = seq_window(p, lane).nt;
+    int total = wave_sum_i(nt);
+    for (int b = 64; b < p.S; b += 64) total += wave_sum_i(seq_window(p, b + lane).nt);
+    total = __builtin_amdgcn_readfirstlane(total) * unit;
+    const int per = max(kMinPieceTiles, (total + p.sk_workers - 1) / p.sk_workers);
+    int start = worker * per;
+    const int end = min(total, start + per);
+    if (start >= end) return;
+    int base = 0;
+    int incl = wave_incl_scan(nt * unit);
+    for (;;) {
+        uint64_t hit = __builtin_amdgcn_ballot_w64(incl > start);
+        while (!hit) {   // the next sequence with tiles lies beyond these 64
+            const int carry = __shfl(incl, 63);
+            base += 64;
+            nt = seq_window(p, base + lane).nt;
+            incl = carry + wave_incl_scan(nt * unit);
+            hit = __builtin_amdgcn_ballot_w64(incl > start);
+        }
+        const int ls = __builtin_ctzll(hit);
+        const int s = base + ls;
+        const SeqWindow w = seq_window(p, s);
+        const int excl = __builtin_amdgcn_readfirstlane(__shfl(incl, ls)) - w.nt * unit;
+        const int off = start - excl;
+        Piece pc;
+        pc.s = s;
+        pc.hk = GROUPED ? hk_fixed : off / w.nt;
+        pc.t0 = GROUPED ? off : off % w.nt;
+        pc.t1 = min(w.nt, pc.t0 + (end - start));
+        const int seg_start = excl + (GROUPED ? 0 : pc.hk * w.nt);
+        pc.seg = GROUPED ? s : s * p.Hkv + pc.hk;
+        pc.rec = worker + pc.seg;
+        pc.pieces = (seg_start + w.nt - 1) / per - seg_start / per + 1;
+        body(w, pc);
+        start = seg_start + pc.t1;
+        if (start >= end) break;
+    }
+}
+
+// Partial record row r of kv head slot hr (0, or the kv head for grouped workers).
+__device__ __forceinline__ float *rec_o(const AttnParams &p, int rec, int hr, int r, int dv) {
+    return p.part_o + (int64_t) rec * p.rec_stride + ((int64_t) hr * p.decode_rows + r) * dv;
+}
+__device__ __forceinline__ float *rec_ml(const AttnParams &p, int rec, int hr, int r) {
+    return p.part_ml + (((int64_t) rec * p.rec_heads + hr) * p.decode_rows + r) * 2;
 }
 
 // Block-table entries of 64 consecutive logical blocks of one sequence, one

@@ -1,9 +1,11 @@
-// pa_decode.hip - split-K paged decode / spec-verify attention for gfx950 (wave64, MFMA).
+// pa_decode.hip - stream-K paged decode / spec-verify attention for gfx950 (wave64, MFMA).
 //
-// One wave per (split, kv head, sequence).  The wave owns every query row of
-// its sequence that maps to the kv head: row r = j*gqa + g for query token j
-// and head g of the GQA group (so the group shares each K/V load), up to 16*NRT
-// rows.  It walks its split's cells in 32-cell tiles straight from the block
+// The grid is a fixed number of single-wave workgroups; wave w takes an equal
+// range of the call's (sequence, kv head, 32-cell tile) line (for_each_piece,
+// pa_common.h), so ragged contexts leave no tail of idle CUs.  Within a
+// piece the wave owns every query row of its sequence that maps to the kv
+// head: row r = j*gqa + g for query token j and head g of the GQA group (so
+// the group shares each K/V load), up to 16*NRT rows.  It walks its piece's cells in 32-cell tiles straight from the block
 // table (no gather):
 //
 //   S^T (32 cells x 16 rows) = K * Q^T     v_mfma_f32_16x16x32_f16, K rows are
@@ -15,16 +17,16 @@
 //                                           operand; V^T B operands are built
 //                                           from 16-byte row loads with v_perm
 //
-// The split's block-table entries are read once into a register (lane i holds
+// The piece's block-table entries are read once into a register (lane i holds
 // logical block first+i) and handed out with lane shuffles, so a tile's loads
 // never wait on a table read.  Loads are single-buffered and phase-pipelined:
 // the next tile's K loads are issued as soon as this tile's QK^T MFMAs have
 // consumed K, its V loads as soon as V has been transposed, so they overlap the
 // softmax and PV work of this tile.
 //
-// Splits write unnormalised partials (O, m, l); pa_merge_kernel combines them
-// with a log-sum-exp merge.  A sequence with a single split writes its output
-// directly.
+// Pieces of a segment cut by worker boundaries write unnormalised partials
+// (O, m, l); pa_merge_kernel combines them with a log-sum-exp merge.  A segment
+// that is one piece writes its output directly.
 // Semantics follow paged_attn_impl (src/iian/paged_attn.cpp:90-146): masks
 // (:124), softcap (:127), all-masked rows -> 0 (:132).
 #include "pa_common.h"
@@ -104,18 +106,16 @@ __device__ __forceinline__ void load_v(const AttnParams &p, const TableWindow &t
     }
 }
 
+// One piece: window tiles [pc.t0, pc.t1) of sequence pc.s at kv head pc.hk.
 template <int D, int NRT>
-__global__ __launch_bounds__(64, (D * NRT <= 128) ? 2 : 1) void pa_decode_f16_kernel(AttnParams p) {
+__device__ __forceinline__ void decode_piece(const AttnParams &p, const SeqWindow &w, const Piece &pc) {
     constexpr int KS = D / 32;
     constexpr int DPL = D / 16;
-    const int split = blockIdx.x, hk = blockIdx.y, s = blockIdx.z;
-    const int lane = threadIdx.x, g = lane >> 4, n = lane & 15;
-    SeqWindow w;
-    seq_window(p, s, w);
+    const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
+    const int s = pc.s, hk = pc.hk;
     const int M = w.nq * p.gqa;
-    if (w.nq <= 0 || M > p.decode_rows || split >= w.nsplit) return;
-    const int cb = w.c_lo + split * w.chunk;
-    const int ce = min(w.c_hi, cb + w.chunk);
+    const int cb = w.c_lo + pc.t0 * kTile;
+    const int ce = min(w.c_hi, w.c_lo + pc.t1 * kTile);
 
     TableWindow tw;
     if (cb < ce) table_load(p, s, cb >> p.bs_log2, w.L, tw);
@@ -157,7 +157,7 @@ __global__ __launch_bounds__(64, (D * NRT <= 128) ? 2 : 1) void pa_decode_f16_ke
             const int next = tile + kTile;
             const bool has_next = next < ce;
             if (has_next && ((min(next + kTile - 1, w.L - 1) >> p.bs_log2) - tw.first) >= 64)
-                table_load(p, s, next >> p.bs_log2, w.L, tw);   // splits longer than 64 blocks
+                table_load(p, s, next >> p.bs_log2, w.L, tw);   // pieces longer than 64 blocks
 
             // S^T = K Q^T for every row tile
             f32x4 sacc[NRT][2];
@@ -248,12 +248,13 @@ __global__ __launch_bounds__(64, (D * NRT <= 128) ? 2 : 1) void pa_decode_f16_ke
         }
     }
 
+    if (pc.t0 == 0 && lane == 0) p.seg_info[pc.seg] = make_int2(pc.rec, pc.pieces);
 #pragma unroll
     for (int rt = 0; rt < NRT; rt++) {
         float l = l_run[rt];
         l += __shfl_xor(l, 16);
         l += __shfl_xor(l, 32);
-        if (w.nsplit == 1) {
+        if (pc.pieces == 1) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int r = rt * 16 + 4 * g + i;
@@ -273,91 +274,95 @@ __global__ __launch_bounds__(64, (D * NRT <= 128) ? 2 : 1) void pa_decode_f16_ke
             for (int i = 0; i < 4; i++) {
                 const int r = rt * 16 + 4 * g + i;
                 if (r < M) {
-                    const int t = w.q0 + r / p.gqa, h = hk * p.gqa + r % p.gqa;
-                    float *op = p.part_o + (part_base(p, s, hk, r, t, h) + split) * D + DPL * n;
+                    float *op = rec_o(p, pc.rec, 0, r, D) + DPL * n;
 #pragma unroll
                     for (int m = 0; m < DPL; m += 4)
                         *(float4 *) (op + m) = make_float4(o[rt][m][i], o[rt][m + 1][i], o[rt][m + 2][i], o[rt][m + 3][i]);
                 }
             }
             const int r = rt * 16 + n;
-            if (g == 0 && r < M) {
-                const int t = w.q0 + r / p.gqa, h = hk * p.gqa + r % p.gqa;
-                float *mp = p.part_ml + (part_base(p, s, hk, r, t, h) + split) * 2;
-                *(float2 *) mp = make_float2(m_run[rt], l);
-            }
+            if (g == 0 && r < M) *(float2 *) rec_ml(p, pc.rec, 0, r) = make_float2(m_run[rt], l);
         }
     }
 }
 
-// Log-sum-exp merge of the split-K partials, one wave per (row, kv head,
-// sequence): out = sum_i 2^(m_i - m) O_i / sum_i 2^(m_i - m) l_i with
-// m = max_i m_i.  A separate launch: the kernel boundary is what makes the
-// partials written on other XCDs visible (their L2s are not coherent within a
-// launch, and a device-scope fence per split costs an L2 write-back).
+template <int D, int NRT>
+__global__ __launch_bounds__(64, (D * NRT <= 128) ? 2 : 1) void pa_decode_f16_kernel(AttnParams p) {
+    for_each_piece<false>(p, blockIdx.x, 0, [&](const SeqWindow &w, const Piece &pc) { decode_piece<D, NRT>(p, w, pc); });
+}
+
+// Log-sum-exp merge of the stream-K partials: one workgroup per (sequence, kv
+// head), wave i merging rows i, i+4, ...: out = sum_j 2^(m_j - m) O_j /
+// sum_j 2^(m_j - m) l_j over the segment's pieces j, m = max_j m_j.  A separate
+// launch: the kernel boundary is what makes the partials written on other XCDs
+// visible (their L2s are not coherent within a launch, and a device-scope
+// fence per piece costs an L2 write-back).
 template <int D>
-__global__ __launch_bounds__(64) void pa_merge_kernel(AttnParams p) {
+__global__ __launch_bounds__(256) void pa_merge_kernel(AttnParams p) {
     constexpr int DL = D / 64;   // dims per lane
-    const int r = blockIdx.x, hk = blockIdx.y, s = blockIdx.z;
-    const int lane = threadIdx.x;
-    SeqWindow w;
-    seq_window(p, s, w);
-    const int M = w.nq * p.gqa;
-    if (w.nq <= 0 || M > p.decode_rows || w.nsplit == 1 || r >= M) return;
-    const int t = w.q0 + r / p.gqa, h = hk * p.gqa + r % p.gqa;
-    const int64_t base = part_base(p, s, hk, r, t, h);
-    const int ns = w.nsplit;
-    // (m, l) of splits lane, lane + 64, ...: the first chunk stays in registers
-    float2 ml0 = make_float2(-INFINITY, 0.f);
-    if (lane < ns) ml0 = *(const float2 *) (p.part_ml + (base + lane) * 2);
-    float mx = ml0.x;
-    for (int sp = lane + 64; sp < ns; sp += 64) mx = fmaxf(mx, p.part_ml[(base + sp) * 2]);
+    const int s = blockIdx.x, hk = blockIdx.y;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int q0 = min(max(p.qsl[s], 0), p.T);
+    const int nq = min(max(p.qsl[s + 1], q0), p.T) - q0;
+    const int M = nq * p.gqa;
+    const bool grouped = p.rec_heads > 1;
+    const int2 info = p.seg_info[grouped ? s : s * p.Hkv + hk];
+    if (nq <= 0 || M > p.decode_rows || info.y <= 1) return;
+    const int hr = grouped ? hk : 0;
+    const int rec0 = info.x, ns = info.y;
+    for (int r = wave; r < M; r += 4) {
+        const int t = q0 + r / p.gqa, h = hk * p.gqa + r % p.gqa;
+        // (m, l) of pieces lane, lane + 64, ...: the first chunk stays in registers
+        float2 ml0 = make_float2(-INFINITY, 0.f);
+        if (lane < ns) ml0 = *(const float2 *) rec_ml(p, rec0 + lane, hr, r);
+        float mx = ml0.x;
+        for (int j = lane + 64; j < ns; j += 64) mx = fmaxf(mx, rec_ml(p, rec0 + j, hr, r)[0]);
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-    float acc[DL];
+        for (int o = 1; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+        float acc[DL];
 #pragma unroll
-    for (int i = 0; i < DL; i++) acc[i] = 0.f;
-    float lpart = 0.f;
-    if (mx != -INFINITY) {
-        for (int c0 = 0; c0 < ns; c0 += 64) {
-            const int nc = min(64, ns - c0);
-            const float2 ml = c0 == 0 ? ml0 : (lane < nc ? *(const float2 *) (p.part_ml + (base + c0 + lane) * 2)
-                                                         : make_float2(-INFINITY, 0.f));
-            const float wl = lane < nc ? __builtin_amdgcn_exp2f(ml.x - mx) : 0.f;   // 0 for an empty split
-            lpart += wl * ml.y;
-            // partial O rows in batches of 8, all loads of a batch issued before use
-            for (int j0 = 0; j0 < nc; j0 += 8) {
-                float v[8][DL];
+        for (int i = 0; i < DL; i++) acc[i] = 0.f;
+        float lpart = 0.f;
+        if (mx != -INFINITY) {
+            for (int c0 = 0; c0 < ns; c0 += 64) {
+                const int nc = min(64, ns - c0);
+                const float2 ml = c0 == 0 ? ml0 : (lane < nc ? *(const float2 *) rec_ml(p, rec0 + c0 + lane, hr, r)
+                                                             : make_float2(-INFINITY, 0.f));
+                const float wl = lane < nc ? __builtin_amdgcn_exp2f(ml.x - mx) : 0.f;   // 0 for an empty piece
+                lpart += wl * ml.y;
+                // partial O rows in batches of 8, all loads of a batch issued before use
+                for (int j0 = 0; j0 < nc; j0 += 8) {
+                    float v[8][DL];
 #pragma unroll
-                for (int u = 0; u < 8; u++) {
-                    const float *op = p.part_o + (base + c0 + min(j0 + u, nc - 1)) * D + lane * DL;
+                    for (int u = 0; u < 8; u++) {
+                        const float *op = rec_o(p, rec0 + c0 + min(j0 + u, nc - 1), hr, r, D) + lane * DL;
 #pragma unroll
-                    for (int i = 0; i < DL; i++) v[u][i] = op[i];
-                }
+                        for (int i = 0; i < DL; i++) v[u][i] = op[i];
+                    }
 #pragma unroll
-                for (int u = 0; u < 8; u++) {
-                    const float wgt = j0 + u < nc ? __shfl(wl, min(j0 + u, 63)) : 0.f;
+                    for (int u = 0; u < 8; u++) {
+                        const float wgt = j0 + u < nc ? __shfl(wl, min(j0 + u, 63)) : 0.f;
 #pragma unroll
-                    for (int i = 0; i < DL; i++) acc[i] += wgt * v[u][i];
+                        for (int i = 0; i < DL; i++) acc[i] += wgt * v[u][i];
+                    }
                 }
             }
         }
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) lpart += __shfl_xor(lpart, o);
+        const float inv = lpart > 0.f ? 1.f / lpart : 0.f;
+        float *out = p.out + ((int64_t) t * p.H + h) * D + lane * DL;
+#pragma unroll
+        for (int i = 0; i < DL; i++) out[i] = acc[i] * inv;
     }
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) lpart += __shfl_xor(lpart, o);
-    const float inv = lpart > 0.f ? 1.f / lpart : 0.f;
-    float *out = p.out + ((int64_t) t * p.H + h) * D + lane * DL;
-#pragma unroll
-    for (int i = 0; i < DL; i++) out[i] = acc[i] * inv;
 }
 
 hipError_t launch_merge(const AttnParams &p, int head_dim, hipStream_t stream) {
-    if (p.max_splits == 1) return hipSuccess;
-    const dim3 grid(p.decode_rows, p.Hkv, p.S);
+    const dim3 grid(p.S, p.Hkv);
     switch (head_dim) {
-        case 64: hipLaunchKernelGGL((pa_merge_kernel<64>), grid, dim3(64), 0, stream, p); break;
-        case 128: hipLaunchKernelGGL((pa_merge_kernel<128>), grid, dim3(64), 0, stream, p); break;
-        case 256: hipLaunchKernelGGL((pa_merge_kernel<256>), grid, dim3(64), 0, stream, p); break;
+        case 64: hipLaunchKernelGGL((pa_merge_kernel<64>), grid, dim3(256), 0, stream, p); break;
+        case 128: hipLaunchKernelGGL((pa_merge_kernel<128>), grid, dim3(256), 0, stream, p); break;
+        case 256: hipLaunchKernelGGL((pa_merge_kernel<256>), grid, dim3(256), 0, stream, p); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -365,8 +370,7 @@ hipError_t launch_merge(const AttnParams &p, int head_dim, hipStream_t stream) {
 
 template <int D, int NRT>
 static hipError_t launch_decode_t(const AttnParams &p, hipStream_t stream) {
-    dim3 grid(p.max_splits, p.Hkv, p.S);
-    hipLaunchKernelGGL((pa_decode_f16_kernel<D, NRT>), grid, dim3(64), 0, stream, p);
+    hipLaunchKernelGGL((pa_decode_f16_kernel<D, NRT>), dim3(p.sk_workers), dim3(64), 0, stream, p);
     const hipError_t e = hipGetLastError();
     return e != hipSuccess ? e : launch_merge(p, D, stream);
 }

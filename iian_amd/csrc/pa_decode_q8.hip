@@ -1,12 +1,15 @@
-// pa_decode_q8.hip - split-K paged decode / spec-verify attention over ggml Q8_0
-// KV pools for gfx950 (wave64, MFMA f16).
+// pa_decode_q8.hip - stream-K paged decode / spec-verify attention over ggml
+// Q8_0 KV pools for gfx950 (wave64, MFMA f16).
 //
 // Pool rows are the reference's Q8_0 rows (ggml-common.h:251-256): a head
 // slice is D/32 blocks of {f16 d, int8 q[32]} = 34*D/32 bytes, only 2-byte
 // aligned inside the row, so it cannot feed MFMA operands straight from
-// memory.  A workgroup owns one (split, kv head, sequence) and has one wave per
-// 16-row query tile (NW = 1, or 2 for spec-verify batches of up to 32 rows per
-// kv head).  Each 32-cell tile is staged once per workgroup:
+// memory.  Workers are groups of Hkv workgroups, one per kv head; group g takes
+// an equal range of the call's (sequence, 32-cell tile) line (for_each_piece,
+// pa_common.h) and each of its workgroups attends that range for its kv head.
+// A workgroup has one wave per 16-row query tile (NW = 1, or 2 for
+// spec-verify batches of up to 32 rows per kv head).  Each 32-cell tile is
+// staged once per workgroup:
 //
 //   raw load   2 lanes per cell, each loads its half of the cell's K or V head
 //              slice as an aligned dword window (issued one tile ahead); with
@@ -24,12 +27,13 @@
 // with q and d exact; rounding happens only where the f16 kernel rounds (q, P).
 //
 // Memory order: a head slice is 34*D/32 bytes, so the slices of neighbouring
-// kv heads share cache lines.  The workgroups of all kv heads of one (split,
-// sequence) pair are therefore dispatched back to back onto one XCD (workgroup
-// id mod 8 selects the XCD), and the loads are ordinary cached loads, so a
-// shared line comes from HBM once and is then hit in that XCD's L2.
+// kv heads share cache lines.  The workgroups of one group are therefore
+// dispatched back to back onto one XCD (workgroup id mod 8 selects the XCD),
+// and the loads are ordinary cached loads, so a shared line comes from HBM
+// once and is then hit in that XCD's L2.
 //
-// Partials and the split-K merge are shared with pa_decode.hip.
+// Partial records (one per piece, all kv heads of the group) and the merge are
+// shared with pa_decode.hip.
 // Semantics follow paged_attn_impl (src/iian/paged_attn.cpp:90-146) run on the
 // dequantised pool (the reference CPU op reaches Q8_0 KV only that way).
 #include "pa_common.h"
@@ -131,26 +135,19 @@ __device__ __forceinline__ f16x8 lds_tr_b16x8_q8(const char *p0, const char *p1)
     return __builtin_bit_cast(f16x8, c);
 }
 
+// One piece of a group: window tiles [pc.t0, pc.t1) of sequence pc.s at kv
+// head pc.hk (workgroup-uniform).
 template <int D, int NW>
-__global__ __launch_bounds__(64 * NW, (D <= 128) ? 2 : 1) void pa_decode_q8_kernel(AttnParams p) {
+__device__ __forceinline__ void q8_piece(const AttnParams &p, Q8Lds<D> &lds, const SeqWindow &w, const Piece &pc) {
     using Q = Q8Shape<D>;
     constexpr int NB = Q::NB, NPV = D / 16, STRIDE = Q::STRIDE;
     constexpr int NRAW = NW == 1 ? 2 : 1;   // pools one wave stages: K and V, or one of them
-    __shared__ Q8Lds<D> lds;
-    // workgroup id -> (kv head, pair = split + max_splits * sequence); see the header comment
-    const int bid = blockIdx.x;
-    const int hk = (bid >> 3) % p.Hkv;
-    const int pair = (bid & 7) + 8 * (bid / (8 * p.Hkv));
-    const int split = pair % p.max_splits, s = pair / p.max_splits;
-    if (s >= p.S) return;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
-    SeqWindow w;
-    seq_window(p, s, w);
+    const int s = pc.s, hk = pc.hk;
     const int M = w.nq * p.gqa;
-    if (w.nq <= 0 || M > p.decode_rows || split >= w.nsplit) return;   // uniform over the workgroup
-    const int cb = w.c_lo + split * w.chunk;
-    const int ce = min(w.c_hi, cb + w.chunk);
+    const int cb = w.c_lo + pc.t0 * kTile;
+    const int ce = min(w.c_hi, w.c_lo + pc.t1 * kTile);
     const bool rows_live = wave * 16 < M;   // this wave's row tile holds query rows
 
     TableWindow tw;
@@ -285,6 +282,7 @@ __global__ __launch_bounds__(64 * NW, (D <= 128) ? 2 : 1) void pa_decode_q8_kern
             }
         }
     }
+    if (pc.t0 == 0 && hk == 0 && threadIdx.x == 0) p.seg_info[pc.seg] = make_int2(pc.rec, pc.pieces);
     if (!rows_live) return;
 
     float l = l_run;
@@ -295,29 +293,37 @@ __global__ __launch_bounds__(64 * NW, (D <= 128) ? 2 : 1) void pa_decode_q8_kern
         const int r = wave * 16 + 4 * g + i;
         const float lr = __shfl(l, 4 * g + i);
         if (r >= M) continue;
-        const int t = w.q0 + r / p.gqa, h = hk * p.gqa + r % p.gqa;
-        if (w.nsplit == 1) {
+        if (pc.pieces == 1) {
+            const int t = w.q0 + r / p.gqa, h = hk * p.gqa + r % p.gqa;
             const float inv = lr > 0.f ? 1.f / lr : 0.f;
             float *op = p.out + ((int64_t) t * p.H + h) * D + n;
 #pragma unroll
             for (int m = 0; m < NPV; m++) op[16 * m] = o[m][i] * inv;
         } else {
-            float *op = p.part_o + (part_base(p, s, hk, r, t, h) + split) * D + n;
+            float *op = rec_o(p, pc.rec, hk, r, D) + n;
 #pragma unroll
             for (int m = 0; m < NPV; m++) op[16 * m] = o[m][i];
         }
     }
-    if (w.nsplit > 1 && g == 0 && qr < M) {
-        const int t = w.q0 + qr / p.gqa, h = hk * p.gqa + qr % p.gqa;
-        float *mp = p.part_ml + (part_base(p, s, hk, qr, t, h) + split) * 2;
-        *(float2 *) mp = make_float2(m_run, l);
-    }
+    if (pc.pieces > 1 && g == 0 && qr < M) *(float2 *) rec_ml(p, pc.rec, hk, qr) = make_float2(m_run, l);
+}
+
+// Workgroup b belongs to group g = (b % 8) + 8 * (b / 8 / Hkv) and kv head
+// (b / 8) % Hkv, so a group's Hkv workgroups share one XCD (b % 8).
+template <int D, int NW>
+__global__ __launch_bounds__(64 * NW, (D <= 128) ? 2 : 1) void pa_decode_q8_kernel(AttnParams p) {
+    __shared__ Q8Lds<D> lds;
+    const int bid = blockIdx.x;
+    const int hk = (bid >> 3) % p.Hkv;
+    const int grp = (bid & 7) + 8 * ((bid >> 3) / p.Hkv);
+    if (grp >= p.sk_workers) return;
+    // every wave of the workgroup runs the same (uniform) plan
+    for_each_piece<true>(p, grp, hk, [&](const SeqWindow &w, const Piece &pc) { q8_piece<D, NW>(p, lds, w, pc); });
 }
 
 template <int D, int NW>
 static hipError_t launch_q8_t(const AttnParams &p, hipStream_t stream) {
-    const int64_t npair = (int64_t) p.max_splits * p.S;
-    const int64_t nwg = 8 * (int64_t) p.Hkv * ((npair + 7) / 8);
+    const int64_t nwg = 8 * (int64_t) p.Hkv * ((p.sk_workers + 7) / 8);
     if (nwg > INT32_MAX) return hipErrorInvalidValue;
     hipLaunchKernelGGL((pa_decode_q8_kernel<D, NW>), dim3((unsigned) nwg), dim3(64 * NW), 0, stream, p);
     const hipError_t e = hipGetLastError();
@@ -325,7 +331,7 @@ static hipError_t launch_q8_t(const AttnParams &p, hipStream_t stream) {
 }
 
 hipError_t launch_decode_q8(const AttnParams &p, int head_dim, hipStream_t stream) {
-    const int nw = p.decode_rows > 16 ? 2 : 1;
+    const int nw = p.decode_rows > 16 ? 2 : 1;   // as q8_waves_per_wg in pa_abi.hip
     switch (head_dim) {
         case 64: return nw == 1 ? launch_q8_t<64, 1>(p, stream) : launch_q8_t<64, 2>(p, stream);
         case 128: return nw == 1 ? launch_q8_t<128, 1>(p, stream) : launch_q8_t<128, 2>(p, stream);

@@ -9,7 +9,7 @@ namespace iian_pa {
 hipError_t launch_decode(const AttnParams &p, int head_dim, int kv_type, hipStream_t stream);
 // The Q8_0-pool variant of launch_decode (pa_decode_q8.hip).
 hipError_t launch_decode_q8(const AttnParams &p, int head_dim, hipStream_t stream);
-// Log-sum-exp merge of the decode kernels' split-K partials (no-op when max_splits == 1).
+// Log-sum-exp merge of the decode kernels' stream-K partial records.
 hipError_t launch_merge(const AttnParams &p, int head_dim, hipStream_t stream);
 // MFMA prefill kernel (sequences with n_q*gqa > p.decode_rows); grid covers max_query_len*gqa rows.
 hipError_t launch_prefill(const AttnParams &p, int head_dim, int kv_type, int max_rows, hipStream_t stream);
