@@ -13,20 +13,26 @@ namespace {
 
 using namespace iian_pa;
 
-// Stream-K workers of the decode kernels (for_each_piece, pa_common.h): the
-// f16 kernel runs kDecodeWaves single-wave workgroups, which is every slot of
-// a 256-CU MI355X at its two waves per SIMD, so each wave's equal share of the
-// call runs at once and the kernel ends with no tail.  The Q8_0 kernel's
-// workers are groups of Hkv workgroups of NW waves over the same wave count.
-constexpr int kDecodeWaves = 2048;
+// Stream-K workers of the decode kernels (for_each_piece, pa_common.h), sized
+// so that every worker's equal share of the call runs at once and the kernel
+// ends with no tail.  The f16 kernel runs one single-wave workgroup per SIMD of
+// a 256-CU MI355X: measured at the Llama-3-8B decode shape, 1024 waves stream
+// the pool faster than 2048 (two per SIMD) or more, and deeper per-wave
+// prefetch gains nothing, so the pool's access pattern, not the number of
+// loads in flight, sets the rate.  The Q8_0 kernel's workers are groups of Hkv
+// workgroups of NW waves over 2048 waves: its LDS staging and conversion want
+// two waves per SIMD (1024 waves measured 1.7x slower at config 4).
+constexpr int kF16DecodeWaves = 1024;
+constexpr int kQ8DecodeWaves = 2048;
+constexpr int kDecodeWaves = kQ8DecodeWaves > kF16DecodeWaves ? kQ8DecodeWaves : kF16DecodeWaves;
 
 int q8_waves_per_wg(int decode_rows) { return decode_rows > 16 ? 2 : 1; }   // NW of pa_decode_q8_kernel
 
 // Workspace: [partial records (numerators)][(m, l) per record row][segment
 // info], each section 256-byte aligned.  Sized for the record count of
 // either kernel at kDecodeRowsMax rows: the f16 kernel has at most
-// kDecodeWaves + S*Hkv one-head records, the Q8_0 kernel at most
-// kDecodeWaves/Hkv + S records of Hkv heads.  A record is padded by 64 floats
+// kF16DecodeWaves + S*Hkv one-head records, the Q8_0 kernel at most
+// kQ8DecodeWaves/Hkv + S records of Hkv heads.  A record is padded by 64 floats
 // so that consecutive records do not sit at a power-of-two stride (rows at
 // such strides alias onto the same HBM channels).
 constexpr int kRecordPad = 64;
@@ -196,10 +202,10 @@ int iian_pa_attention(void *stream, const float *q, const void *k_pool, const vo
 
     if (type_k == IIAN_PA_TYPE_Q8_0) {
         p.rec_heads = n_head_kv;
-        p.sk_workers = std::max(1, kDecodeWaves / (q8_waves_per_wg(p.decode_rows) * n_head_kv));
+        p.sk_workers = std::max(1, kQ8DecodeWaves / (q8_waves_per_wg(p.decode_rows) * n_head_kv));
     } else {
         p.rec_heads = 1;
-        p.sk_workers = kDecodeWaves;
+        p.sk_workers = kF16DecodeWaves;
     }
     p.rec_stride = (int64_t) p.rec_heads * p.decode_rows * head_dim_v + kRecordPad;
     const WorkspaceLayout wl = workspace_layout(n_seqs, n_head_kv, head_dim_v);

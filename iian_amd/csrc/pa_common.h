@@ -162,7 +162,8 @@ __device__ __forceinline__ void for_each_piece(const AttnParams &p, int worker, 
     const int lane = threadIdx.x & 63;
     const int unit = GROUPED ? 1 : p.Hkv;
     // lanes hold the tile counts of sequences base + lane and their inclusive
-    // prefix along the line
+    // prefix along the line; a piece's window is re-read with scalar loads
+    // (keeping every field in lanes costs registers the tile loop needs)
     int nt = seq_window(p, lane).nt;
     int total = wave_sum_i(nt);
     for (int b = 64; b < p.S; b += 64) total += wave_sum_i(seq_window(p, b + lane).nt);

@@ -286,6 +286,9 @@ __device__ __forceinline__ void decode_piece(const AttnParams &p, const SeqWindo
     }
 }
 
+// One wave per SIMD is launched (kF16DecodeWaves in pa_abi.hip), but the
+// register budget stays at two waves per SIMD up to D*NRT = 128: in a mixed
+// batch these waves share the CUs with the prefill kernel's workgroups.
 template <int D, int NRT>
 __global__ __launch_bounds__(64, (D * NRT <= 128) ? 2 : 1) void pa_decode_f16_kernel(AttnParams p) {
     for_each_piece<false>(p, blockIdx.x, 0, [&](const SeqWindow &w, const Piece &pc) { decode_piece<D, NRT>(p, w, pc); });
@@ -312,7 +315,15 @@ __global__ __launch_bounds__(256) void pa_merge_kernel(AttnParams p) {
     const int rec0 = info.x, ns = info.y;
     for (int r = wave; r < M; r += 4) {
         const int t = q0 + r / p.gqa, h = hk * p.gqa + r % p.gqa;
-        // (m, l) of pieces lane, lane + 64, ...: the first chunk stays in registers
+        // the first 8 partial O rows are loaded together with the (m, l) of
+        // pieces lane, lane + 64, ...; the first (m, l) chunk stays in registers
+        float v0[8][DL];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const float *op = rec_o(p, rec0 + min(u, ns - 1), hr, r, D) + lane * DL;
+#pragma unroll
+            for (int i = 0; i < DL; i++) v0[u][i] = op[i];
+        }
         float2 ml0 = make_float2(-INFINITY, 0.f);
         if (lane < ns) ml0 = *(const float2 *) rec_ml(p, rec0 + lane, hr, r);
         float mx = ml0.x;
@@ -333,11 +344,18 @@ __global__ __launch_bounds__(256) void pa_merge_kernel(AttnParams p) {
                 // partial O rows in batches of 8, all loads of a batch issued before use
                 for (int j0 = 0; j0 < nc; j0 += 8) {
                     float v[8][DL];
+                    if (c0 == 0 && j0 == 0) {
 #pragma unroll
-                    for (int u = 0; u < 8; u++) {
-                        const float *op = rec_o(p, rec0 + c0 + min(j0 + u, nc - 1), hr, r, D) + lane * DL;
+                        for (int u = 0; u < 8; u++)
 #pragma unroll
-                        for (int i = 0; i < DL; i++) v[u][i] = op[i];
+                            for (int i = 0; i < DL; i++) v[u][i] = v0[u][i];
+                    } else {
+#pragma unroll
+                        for (int u = 0; u < 8; u++) {
+                            const float *op = rec_o(p, rec0 + c0 + min(j0 + u, nc - 1), hr, r, D) + lane * DL;
+#pragma unroll
+                            for (int i = 0; i < DL; i++) v[u][i] = op[i];
+                        }
                     }
 #pragma unroll
                     for (int u = 0; u < 8; u++) {
