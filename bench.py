@@ -32,6 +32,8 @@ WORKLOADS = {
             "16-token f16 blocks in a 65536-block pool, + KV write of 64 tokens",
     "cfg3": "Qwen3-8B mixed batch, H32/Hkv8/D128: 4 prefill chunks x 512 over prior U[1024,4096] "
             "(1024-token shared prefix) + 32 decode tokens, f16 KV",
+    "cfg3_prefill": "Qwen3-8B, H32/Hkv8/D128: the 4 prefill chunks of cfg3 alone (x 512 tokens over prior "
+                    "U[1024,4096], 1024-token shared prefix), f16 KV",
     "cfg4": "Llama-3-8B Q8_0 KV, 128 seqs x 4096 prior + 5 spec-verify queries",
     "cfg5_global_decode": "Gemma3-12B global layer decode, H16/Hkv8/D256, 32 seqs, ctx U[8192,32768]",
     "cfg5_local_decode": "Gemma3-12B local layer decode (n_swa=1024), H16/Hkv8/D256, 32 seqs",

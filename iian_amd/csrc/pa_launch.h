@@ -13,6 +13,8 @@ hipError_t launch_decode_q8(const AttnParams &p, int head_dim, hipStream_t strea
 hipError_t launch_merge(const AttnParams &p, int head_dim, hipStream_t stream);
 // MFMA prefill kernel (sequences with n_q*gqa > p.decode_rows); grid covers max_query_len*gqa rows.
 hipError_t launch_prefill(const AttnParams &p, int head_dim, int kv_type, int max_rows, hipStream_t stream);
+// The 16-row-tile prefill kernel (pa_prefill16.hip), used at head size 256.
+hipError_t launch_prefill16(const AttnParams &p, int head_dim, int kv_type, int max_rows, hipStream_t stream);
 
 hipError_t launch_kv_write(const float *rows, int64_t n_rows, int64_t row_elems, const int64_t *slots, void *pool,
                            int64_t n_cells, int type, int32_t *err, hipStream_t stream);

@@ -1,0 +1,74 @@
+// pa_mfma.h - MFMA 32x32x16 and LDS tile helpers shared by the gfx950 prefill kernels.
+//
+// MFMA 32x32x16 operand layouts (lane l, h = l/32): A[m][k] holds
+// A[l%32][8h .. 8h+7]; B holds B[8h .. 8h+7][l%32]; the f32 result register r
+// holds D[8(r/4) + 4h + r%4][l%32].
+#pragma once
+
+#include "pa_common.h"
+
+namespace iian_pa {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+
+// LDS tile layouts.  Register-staged tiles (Q8_0 pools, D = 64) use padded
+// rows: the QK^T A operand reads 16 consecutive K rows per 16 lanes, each 4
+// banks after the last; a V transpose read covers 4 rows x 32 bytes per 16
+// lanes, rows 16 banks apart so the two dim halves of a lane half never share
+// a bank.  Tiles loaded straight into LDS (f16 pools at D >= 128) fill 1 KB
+// per wave instruction, so their rows are unpadded and the 16-byte chunks of
+// row r are XOR-permuted by swz(r) instead: 16 consecutive rows read at one
+// logical chunk hit 16 different chunk slots, and the 4 rows of a transpose
+// read (two chunks each, both dim halves) hit 16 different ones.
+template <int D, bool DMA>
+struct PrefillShape {
+    // cells per tile: 64 (two independent 32-cell S^T halves) up to D = 128;
+    // 32 at D = 256, where a second half's scores would not fit in registers
+    static constexpr int PT = D <= 128 ? 64 : 32;
+    static constexpr int NH = PT / 32;                         // 32-cell halves per tile
+    static constexpr int KK = D / 16;                          // QK^T k-steps (16 dims each)
+    static constexpr int NO = D / 32;                          // PV output tiles (32 dims each)
+    static constexpr int KSTRIDE = DMA ? D * 2 : D * 2 + 16;
+    static constexpr int VSTRIDE = DMA ? D * 2 : D * 2 + 64;
+    static constexpr int KBYTES = PT * KSTRIDE;
+    static constexpr int VBYTES = PT * VSTRIDE;
+    static constexpr int CHUNKS = PT * (D / 8);                // 16-byte chunks per tile per tensor
+};
+
+__device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+
+// Byte offset in a tile of byte `b` of row r.
+template <int D, bool DMA>
+__device__ __forceinline__ int tile_off(int r, int b, int stride) {
+    if constexpr (DMA) return r * stride + ((((b >> 4) ^ swz(r & 15)) << 4) | (b & 15));
+    else return r * stride + b;
+}
+
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+__device__ __forceinline__ f16x8 lds_tr_b16x8(const char *p0, const char *p1) {
+    const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *) (uintptr_t) p0);
+    const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *) (uintptr_t) p1);
+    typedef short s16x8 __attribute__((ext_vector_type(8)));
+    const s16x8 c = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+    return __builtin_bit_cast(f16x8, c);
+}
+
+// 16 bytes per lane from global memory straight into LDS: lane i's bytes land
+// at LDS byte lds_off + 16i (global_load_lds_dwordx4, LDS base in m0, latched
+// at issue).  Issued from inline assembly on purpose: the compiler treats its
+// own LDS-load builtin as a write to all of LDS and waits for every one in
+// flight before any later LDS read, which would serialise a double-buffered
+// tile stream.  Callers order the loads themselves: s_waitcnt vmcnt(0) and a
+// workgroup barrier before the tile is read, and a barrier between the last
+// read of a buffer and the loads that refill it.
+__device__ __forceinline__ void lds_load16(const void *gptr, uint32_t lds_off) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_off), "v"(gptr) : "m0");
+}
+
+__device__ __forceinline__ f32x16 mfma32(const f16x8 &a, const f16x8 &b, const f32x16 &c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+}  // namespace iian_pa

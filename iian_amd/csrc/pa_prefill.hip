@@ -1,74 +1,75 @@
-// pa_prefill.hip - chunked-prefill causal paged attention for gfx950 (MFMA f16, LDS-staged KV).
+// pa_prefill.hip - chunked-prefill causal paged attention for gfx950 (MFMA 32x32x16 f16, LDS-staged KV).
 //
 // One workgroup of NW waves per (row block, kv head, sequence); rows are
-// r = j*gqa + g (query token j, head g of the GQA group), NRT 16-row MFMA tiles
-// per wave.  The workgroup streams the sequence's cells in 32-cell tiles
+// r = j*gqa + g (query token j, head g of the GQA group) and every wave owns 32
+// of them.  The workgroup streams the sequence's cells in 64-cell tiles
 // through the block table into LDS (register-staged double buffer) and every
-// wave reuses each tile for all its rows:
+// wave reuses each tile for its 32 rows:
 //
-//   S^T = K * Q^T       v_mfma_f32_16x16x32_f16, K rows read from LDS with
-//                       ds_read_b128 as the A operand, Q^T from registers
-//   online softmax      exp2 domain; causal / sliding-window masks only on
-//                       tiles that straddle a boundary; waves skip tiles that
-//                       are fully masked for all their rows
-//   O += P * V          P from registers (A operand); V^T B operands come
-//                       straight from the row-major LDS tile through the
+//   S^T = K * Q^T       v_mfma_f32_32x32x16_f16: K rows (cells) from LDS with
+//                       ds_read_b128 as the A operand, Q^T (f16 hi/lo pair)
+//                       from registers as the B operand; the tile's two
+//                       32-cell halves are two independent accumulation chains
+//   online softmax      exp2 domain; lane l holds 32 cells of query row l%32,
+//                       lane l^32 the other 32; causal / sliding-window masks
+//                       only on tiles that straddle a boundary; waves skip
+//                       tiles that are fully masked for all their rows
+//   O += P * V          P straight from the S^T registers as the A operand (the
+//                       k positions of a PV step are the cells the lane holds);
+//                       V B operands from the row-major LDS tile through the
 //                       gfx950 transpose read ds_read_b64_tr_b16
+//
+// 32 rows per wave halve the LDS bytes read per flop against 16-row tiles.
+// A chain of dependent MFMAs issues at ~64% of the MFMA rate on MI355X
+// (measured: one 32x32x16 accumulator per wave 1.58 PFLOP/s, two 2.11, four
+// 2.44), so a tile carries two independent S^T chains and PV four output tiles.
+//
+// MFMA 32x32x16 operand layouts (lane l, h = l/32): A[m][k] holds
+// A[l%32][8h .. 8h+7]; B holds B[8h .. 8h+7][l%32]; the f32 result register r
+// holds D[8(r/4) + 4h + r%4][l%32].
 //
 // Workgroups of one (kv head, sequence) share their K/V and are placed on one
 // XCD (its L2) by remapping the linear workgroup id.
 // Semantics: paged_attn_impl (src/iian/paged_attn.cpp:90-146).
 #include "pa_common.h"
 #include "pa_launch.h"
+#include "pa_mfma.h"
 
 namespace iian_pa {
 
+// Waves per SIMD asked of the register allocator: two at D <= 128 (two 4-wave
+// workgroups per CU in 256 registers), one at D = 256 (O and the q pair take
+// 256 registers alone).
 template <int D>
-struct PrefillShape {
-    static constexpr int KS = D / 32;                 // QK^T k-steps
-    static constexpr int NPV = D / 16;                // PV MFMAs (16 output dims each)
-    // Padded LDS rows, both tiles stored in the order their readers walk the
-    // cells: LDS row 16h + 4j + i holds cell 8j + 4h + i.  The QK^T A operand
-    // (half h) then reads 16 consecutive K rows, each 4 banks after the last,
-    // and a V transpose read (cells 8g + i, then 8g + 4 + i) reads rows 4g + i
-    // (resp. 16 + 4g + i), 32 bytes each, 8 banks apart.
-    static constexpr int KSTRIDE = D * 2 + 16;
-    static constexpr int VSTRIDE = D * 2 + 32;
-    static constexpr int TILE_BYTES = kTile * VSTRIDE;
-    static constexpr int CHUNKS = kTile * (D / 8);    // 16-byte chunks per tile per tensor
+struct PrefillOcc {
+    static constexpr int kWavesPerSimd = D <= 128 ? 2 : 1;
 };
-
-typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-
-__device__ __forceinline__ f16x8 lds_tr_b16x8(const char *p0, const char *p1) {
-    const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *) (uintptr_t) p0);
-    const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *) (uintptr_t) p1);
-    typedef short s16x8 __attribute__((ext_vector_type(8)));
-    const s16x8 c = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-    return __builtin_bit_cast(f16x8, c);
-}
 
 // KVT: pool type, 1 = f16, 8 = ggml Q8_0 (ggml-common.h:251-256).  A Q8_0 tile
 // is staged with one thread per (tensor, cell, block): K as its exact int8
 // values in f16 plus the block scales d as f32 in LDS, applied per cell after
-// each QK^T k-step MFMA (k-step = block), so q*d enters the scores exactly;
-// V as f16(q*d), the correctly rounded dequantised value.
-template <int D, int NRT, int NW, int KVT>
-// Waves per SIMD asked of the register allocator: four for f16 at D = 128 (two
-// 8-wave workgroups per CU in 128 VGPRs), else two up to D = 128, one at 256.
-__global__ __launch_bounds__(NW * 64, (D == 128 && KVT == 1) ? 4 : (D <= 128 ? 2 : 1)) void pa_prefill_kernel(
-    AttnParams p, int n_rb) {
-    using SH = PrefillShape<D>;
-    constexpr int KS = SH::KS, NPV = SH::NPV, KSTRIDE = SH::KSTRIDE, VSTRIDE = SH::VSTRIDE;
+// the two QK^T k-steps of each block, so q*d enters the scores exactly; V as
+// f16(q*d), the correctly rounded dequantised value.
+template <int D, int NW, int KVT>
+__global__ __launch_bounds__(NW * 64, PrefillOcc<D>::kWavesPerSimd) void pa_prefill_kernel(AttnParams p, int n_rb) {
+    constexpr bool DMA = KVT == 1 && D >= 128;   // f16 tiles loaded straight into LDS
+    using SH = PrefillShape<D, DMA>;
+    constexpr int KK = SH::KK, NO = SH::NO, KSTRIDE = SH::KSTRIDE, VSTRIDE = SH::VSTRIDE;
+    constexpr int PT = SH::PT, NH = SH::NH, NS = 16 * NH;   // cells per tile, 32-cell halves, scores per lane
     constexpr bool Q8 = KVT == 8;
-    constexpr int CPT = SH::CHUNKS / (NW * 64);   // f16: 16-byte chunks per thread per tensor
-    static_assert(Q8 || CPT * NW * 64 == SH::CHUNKS, "tile chunks must divide evenly");
+    constexpr int NT = NW * 64;
+    constexpr int CPT = SH::CHUNKS / NT;          // f16: 16-byte chunks per thread per tensor
+    static_assert(Q8 || CPT * NT == SH::CHUNKS, "tile chunks must divide evenly");
     constexpr int NB = D / 32;                    // Q8_0 blocks per head slice
-    constexpr int ITEMS = 2 * kTile * NB;         // Q8_0: (tensor, cell, block) staging items
-    static_assert(!Q8 || ITEMS <= NW * 64, "one Q8_0 staging item per thread");
-    constexpr int ROWS = NW * NRT * 16;
-    __shared__ __attribute__((aligned(16))) char lds[2][2][SH::TILE_BYTES];
-    __shared__ __attribute__((aligned(16))) float ksc[2][Q8 ? NB : 1][kTile];   // Q8_0 K scales [block][cell]
+    constexpr int ITEMS = 2 * PT * NB;        // Q8_0: (tensor, cell, block) staging items
+    constexpr int IPT = (ITEMS + NT - 1) / NT;    // Q8_0 items per thread
+    constexpr int ROWS = NW * 32;
+    // double-buffered K/V tiles
+    __shared__ __attribute__((aligned(16))) char lds_k0[SH::KBYTES];
+    __shared__ __attribute__((aligned(16))) char lds_k1[SH::KBYTES];
+    __shared__ __attribute__((aligned(16))) char lds_v0[SH::VBYTES];
+    __shared__ __attribute__((aligned(16))) char lds_v1[SH::VBYTES];
+    __shared__ __attribute__((aligned(16))) float ksc[2][Q8 ? NB : 1][PT];   // Q8_0 K scales [block][cell]
 
     // XCD-aware mapping: workgroups are dispatched round-robin over the 8 XCDs
     // (bid % 8).  (sequence, kv head) pairs are dealt round-robin to XCDs and
@@ -83,7 +84,7 @@ __global__ __launch_bounds__(NW * 64, (D == 128 && KVT == 1) ? 4 : (D <= 128 ? 2
     const int s = pair / p.Hkv;
     const int hk = pair % p.Hkv;
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, n = lane & 15;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hh = lane >> 5, n = lane & 31;
     const int L = p.seq_lens[s];
     const int q0 = min(max(p.qsl[s], 0), p.T);
     const int nq = min(max(p.qsl[s + 1], q0), p.T) - q0;
@@ -93,7 +94,7 @@ __global__ __launch_bounds__(NW * 64, (D == 128 && KVT == 1) ? 4 : (D <= 128 ? 2
     if (R0 >= M) return;
 
     // positions of this workgroup's and this wave's rows
-    const int Rw = R0 + wave * NRT * 16;
+    const int Rw = R0 + wave * 32;
     int wg_min = INT32_MAX, wg_max = INT32_MIN, w_min = INT32_MAX, w_max = INT32_MIN;
     {
         const int j0 = R0 / p.gqa, j1 = (min(M, R0 + ROWS) - 1) / p.gqa;
@@ -103,7 +104,7 @@ __global__ __launch_bounds__(NW * 64, (D == 128 && KVT == 1) ? 4 : (D <= 128 ? 2
             wg_max = max(wg_max, ps);
         }
         if (Rw < M) {
-            const int k0 = Rw / p.gqa, k1 = (min(M, Rw + NRT * 16) - 1) / p.gqa;
+            const int k0 = Rw / p.gqa, k1 = (min(M, Rw + 32) - 1) / p.gqa;
             for (int j = k0 + lane; j <= k1; j += 64) {
                 const int ps = p.pos[q0 + j];
                 w_min = min(w_min, ps);
@@ -124,34 +125,30 @@ __global__ __launch_bounds__(NW * 64, (D == 128 && KVT == 1) ? 4 : (D <= 128 ? 2
     if (p.n_swa > 0) c_lo = max(0, wg_min - p.n_swa + 1);
     c_lo &= ~(kTile - 1);
 
-    // Q^T B operands (pre-scaled f16 hi/lo pairs; measured: +4-6% time, the
-    // score error of a single f16 q removed), row positions, running state
-    f16x8 qv[NRT][KS], ql[NRT][KS];
-    int prow[NRT];
-    float m_run[NRT], l_run[NRT];
-    f32x4 o[NRT][NPV];
+    // Q^T B operands of query row n (pre-scaled f16 hi/lo pairs, dims
+    // 16kk + 8hh .. +7), its position and running state.  The pair carries q
+    // to ~2^-22 relative (split_f16x8).
+    f16x8 qv[KK], ql[KK];
+    const int qr = Rw + n;
+    int prow = wave_live ? w_max : 0;
+    if (qr < M) {
+        const int t = q0 + qr / p.gqa, h = hk * p.gqa + qr % p.gqa;
+        prow = p.pos[t];
+        const float *qp = p.q + ((int64_t) t * p.H + h) * D + 8 * hh;
 #pragma unroll
-    for (int rt = 0; rt < NRT; rt++) {
-        const int r = Rw + rt * 16 + n;
-        prow[rt] = wave_live ? w_max : 0;
-        if (r < M) {
-            const int t = q0 + r / p.gqa, h = hk * p.gqa + r % p.gqa;
-            prow[rt] = p.pos[t];
-            const float *qp = p.q + ((int64_t) t * p.H + h) * D + 8 * g;
+        for (int kk = 0; kk < KK; kk++)
+            split_f16x8(*(const float4 *) (qp + 16 * kk), *(const float4 *) (qp + 16 * kk + 4), p.qscale, qv[kk],
+                        ql[kk]);
+    } else {
 #pragma unroll
-            for (int ks = 0; ks < KS; ks++)
-                split_f16x8(*(const float4 *) (qp + 32 * ks), *(const float4 *) (qp + 32 * ks + 4), p.qscale,
-                            qv[rt][ks], ql[rt][ks]);
-        } else {
-#pragma unroll
-            for (int ks = 0; ks < KS; ks++)
-                qv[rt][ks] = ql[rt][ks] = __builtin_bit_cast(f16x8, u32x4{0u, 0u, 0u, 0u});
-        }
-        m_run[rt] = -INFINITY;
-        l_run[rt] = 0.f;
-#pragma unroll
-        for (int m = 0; m < NPV; m++) o[rt][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int kk = 0; kk < KK; kk++) qv[kk] = ql[kk] = __builtin_bit_cast(f16x8, u32x4{0u, 0u, 0u, 0u});
     }
+    float m_run = -INFINITY, l_run = 0.f;   // of query row n (same in lanes n and n + 32)
+    f32x16 o[NO];                           // O rows 8(r/4) + 4hh + r%4, dims 32m + n
+#pragma unroll
+    for (int m = 0; m < NO; m++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) o[m][r] = 0.f;
 
     const int bs_mask = (1 << p.bs_log2) - 1;
     const int64_t head_off = (int64_t) hk * D * 2;
@@ -159,30 +156,33 @@ __global__ __launch_bounds__(NW * 64, (D == 128 && KVT == 1) ? 4 : (D <= 128 ? 2
     // lane shuffles: a tile's loads never wait on a table read
     TableWindow tw;
     if (c_lo < c_hi) table_load(p, s, c_lo >> p.bs_log2, L, tw);
-    u32x4 kst[Q8 ? 1 : CPT], vst[Q8 ? 1 : CPT];
-    // Q8_0 item of this thread: tensor (0 = K), cell and block; its 34 bytes
+    u32x4 kst[(Q8 || DMA) ? 1 : CPT], vst[(Q8 || DMA) ? 1 : CPT];
+    // Q8_0 items of this thread: tensor (0 = K), cell and block; its 34 bytes
     // sit 2 bytes into (odd block) or at the start of (even block) an aligned
     // 9-dword window that stays inside the head slice
-    const int qi_t = tid / (kTile * NB), qi_cell = (tid % (kTile * NB)) / NB, qi_b = tid % NB;
-    const bool qi_live = Q8 && tid < ITEMS;
-    uint32_t qraw[9];
+    uint32_t qraw[Q8 ? IPT : 1][9];
     auto load_global = [&](int tile) {
-        if (((min(tile + kTile - 1, L - 1) >> p.bs_log2) - tw.first) >= 64) table_load(p, s, tile >> p.bs_log2, L, tw);
+        if (((min(tile + PT - 1, L - 1) >> p.bs_log2) - tw.first) >= 64) table_load(p, s, tile >> p.bs_log2, L, tw);
         if constexpr (Q8) {
-            const int c = min(tile + qi_cell, L - 1);
-            const int32_t blk = __shfl(tw.id, (c >> p.bs_log2) - tw.first);
-            const int64_t row = ((int64_t) blk << p.bs_log2) | (c & bs_mask);
-            if (qi_live) {
-                const int start = hk * NB * 34 + 34 * qi_b;
-                const uint32_t *src = (const uint32_t *) ((qi_t ? p.v_pool + row * p.v_row : p.k_pool + row * p.k_row) +
-                                                          (start & ~3));
 #pragma unroll
-                for (int i = 0; i < 9; i++) qraw[i] = src[i];
+            for (int it = 0; it < IPT; it++) {
+                const int item = tid + it * NT;
+                const int qi_t = item / (PT * NB), qi_cell = (item % (PT * NB)) / NB, qi_b = item % NB;
+                const int c = min(tile + qi_cell, L - 1);
+                const int32_t blk = __shfl(tw.id, (c >> p.bs_log2) - tw.first);
+                const int64_t row = ((int64_t) blk << p.bs_log2) | (c & bs_mask);
+                if (item < ITEMS) {
+                    const int start = hk * NB * 34 + 34 * qi_b;
+                    const uint32_t *src = (const uint32_t *) ((qi_t ? p.v_pool + row * p.v_row
+                                                                     : p.k_pool + row * p.k_row) + (start & ~3));
+#pragma unroll
+                    for (int i = 0; i < 9; i++) qraw[it][i] = src[i];
+                }
             }
-        } else {
+        } else if constexpr (!DMA) {
 #pragma unroll
             for (int j = 0; j < CPT; j++) {
-                const int q = tid + j * NW * 64;
+                const int q = tid + j * NT;
                 const int cell = q / (D / 8), col = q % (D / 8);
                 const int c = min(tile + cell, L - 1);
                 const int32_t blk = __shfl(tw.id, (c >> p.bs_log2) - tw.first);
@@ -192,197 +192,292 @@ __global__ __launch_bounds__(NW * 64, (D == 128 && KVT == 1) ? 4 : (D <= 128 ? 2
             }
         }
     };
+    // DMA tiles: wave instruction q of a tensor fills tile bytes [1024q, 1024q + 1024);
+    // lane i's 16 bytes land at 1024q + 16i = row r, chunk slot (16i % 2D)/16,
+    // which holds the row's logical chunk slot ^ swz(r)
+    auto load_dma = [&](int tile, char *Kd, char *Vd) {
+        if (((min(tile + PT - 1, L - 1) >> p.bs_log2) - tw.first) >= 64) table_load(p, s, tile >> p.bs_log2, L, tw);
+        constexpr int NQ = SH::KBYTES / 1024 / NW;   // instructions per wave per tensor
+#pragma unroll
+        for (int j = 0; j < NQ; j++) {
+            const int q = j * NW + wave;
+            const int b = q * 1024 + 16 * lane;
+            const int r = b / (2 * D), slot = (b % (2 * D)) >> 4;
+            const int c = min(tile + r, L - 1);
+            const int32_t blk = __shfl(tw.id, (c >> p.bs_log2) - tw.first);
+            const int64_t row = ((int64_t) blk << p.bs_log2) | (c & bs_mask);
+            const int64_t col = head_off + 16 * (slot ^ swz(r & 15));
+            const uint32_t lk = __builtin_amdgcn_readfirstlane((uint32_t) (uintptr_t) (Kd + q * 1024));
+            const uint32_t lv = __builtin_amdgcn_readfirstlane((uint32_t) (uintptr_t) (Vd + q * 1024));
+            lds_load16(p.k_pool + row * p.k_row + col, lk);
+            lds_load16(p.v_pool + row * p.v_row + col, lv);
+        }
+    };
     auto store_lds = [&](int buf) {
         if constexpr (Q8) {
-            if (!qi_live) return;
-            const int lrow = ((qi_cell >> 2) & 1) * 16 + (qi_cell >> 3) * 4 + (qi_cell & 3);
-            const bool odd = qi_b & 1;   // block starts 2 bytes into the window
-            const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t) (odd ? qraw[0] >> 16 : qraw[0]));
-            typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
-            const f16x2_t d2 = {d, d};
-            u32x4 h[4];
 #pragma unroll
-            for (int k = 0; k < 8; k++) {
-                const uint32_t q4 = odd ? qraw[k + 1] : __builtin_amdgcn_alignbyte(qraw[k + 1], qraw[k], 2);
-                uint32_t lo, hi;
-                i8x4_to_f16(q4, lo, hi);
-                if (qi_t) {   // V: f16(q*d)
-                    lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2_t, lo) * d2);
-                    hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2_t, hi) * d2);
+            for (int it = 0; it < IPT; it++) {
+                const int item = tid + it * NT;
+                if (item >= ITEMS) continue;
+                const int qi_t = item / (PT * NB), qi_cell = (item % (PT * NB)) / NB, qi_b = item % NB;
+                const bool odd = qi_b & 1;   // block starts 2 bytes into the window
+                const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t) (odd ? qraw[it][0] >> 16 : qraw[it][0]));
+                typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+                const f16x2_t d2 = {d, d};
+                u32x4 hv[4];
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    const uint32_t q4 = odd ? qraw[it][k + 1] : __builtin_amdgcn_alignbyte(qraw[it][k + 1], qraw[it][k], 2);
+                    uint32_t lo, hi;
+                    i8x4_to_f16(q4, lo, hi);
+                    if (qi_t) {   // V: f16(q*d)
+                        lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2_t, lo) * d2);
+                        hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2_t, hi) * d2);
+                    }
+                    hv[k >> 1][2 * (k & 1)] = lo;
+                    hv[k >> 1][2 * (k & 1) + 1] = hi;
                 }
-                h[k >> 1][2 * (k & 1)] = lo;
-                h[k >> 1][2 * (k & 1) + 1] = hi;
-            }
-            char *dst = qi_t ? &lds[buf][1][lrow * VSTRIDE + qi_b * 64] : &lds[buf][0][lrow * KSTRIDE + qi_b * 64];
+                char *dst = qi_t ? (buf ? lds_v1 : lds_v0) + qi_cell * VSTRIDE + qi_b * 64
+                                 : (buf ? lds_k1 : lds_k0) + qi_cell * KSTRIDE + qi_b * 64;
 #pragma unroll
-            for (int k = 0; k < 4; k++) *(u32x4 *) (dst + 16 * k) = h[k];
-            if (!qi_t) ksc[buf][qi_b][qi_cell] = (float) d;
-        } else {
+                for (int k = 0; k < 4; k++) *(u32x4 *) (dst + 16 * k) = hv[k];
+                if (!qi_t) ksc[buf][qi_b][qi_cell] = (float) d;
+            }
+        } else if constexpr (!DMA) {
 #pragma unroll
             for (int j = 0; j < CPT; j++) {
-                const int q = tid + j * NW * 64;
+                const int q = tid + j * NT;
                 const int cell = q / (D / 8), col = q % (D / 8);
-                const int lrow = ((cell >> 2) & 1) * 16 + (cell >> 3) * 4 + (cell & 3);
-                *(u32x4 *) (&lds[buf][0][lrow * KSTRIDE + col * 16]) = kst[j];
-                *(u32x4 *) (&lds[buf][1][lrow * VSTRIDE + col * 16]) = vst[j];
+                *(u32x4 *) ((buf ? lds_k1 : lds_k0) + cell * KSTRIDE + col * 16) = kst[j];
+                *(u32x4 *) ((buf ? lds_v1 : lds_v0) + cell * VSTRIDE + col * 16) = vst[j];
             }
         }
     };
 
-    auto compute = [&](int tile, int buf) {
+    auto compute = [&](int tile, int buf, const char *Kl, const char *Vl) {
         if (!wave_live) return;
-        if (p.causal && tile > w_max) return;                              // every cell after every row
-        if (p.n_swa > 0 && tile + kTile - 1 <= w_min - p.n_swa) return;   // every cell out of every window
-        const bool full = tile + kTile <= L && (!p.causal || tile + kTile - 1 <= w_min) &&
+        if (p.causal && tile > w_max) return;                               // every cell after every row
+        if (p.n_swa > 0 && tile + PT - 1 <= w_min - p.n_swa) return;   // every cell out of every window
+        const bool full = tile + PT <= L && (!p.causal || tile + PT - 1 <= w_min) &&
                           (p.n_swa <= 0 || w_max - tile < p.n_swa);
-        const char *Kl = lds[buf][0];
-        const char *Vl = lds[buf][1];
-        f16x8 ka[2][KS];
+
+        // S^T = K Q^T for the tile's two 32-cell halves (independent chains;
+        // the hi and lo products of a half accumulate in its chain).  Register
+        // r of half c holds cell 32c + 8(r/4) + 4hh + r%4.
+        // The accumulators start at -mofs, the row's reference max, so that a
+        // full tile's scores come out relative to it and feed exp2 directly
+        // (not with a softcap, which must see the raw score).
+        const float mofs = (p.softcap > 0.f || m_run == -INFINITY) ? 0.f : m_run;
+        f32x16 sa[NH];
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            // A operand row n of half h = cell 8(n/4) + 4h + n%4 = LDS row 16h + n
+        for (int c = 0; c < NH; c++)
 #pragma unroll
-            for (int ks = 0; ks < KS; ks++)
-                ka[h][ks] = *(const f16x8 *) (Kl + (16 * h + n) * KSTRIDE + (32 * ks + 8 * g) * 2);
-        }
-        f16x8 pa[NRT];
+            for (int r = 0; r < 16; r++) sa[c][r] = -mofs;
+        // A row = cell 32c + n, dims 16kk + 8hh (tile bytes 32kk + 16hh)
+        if constexpr (Q8) {
+            // k-steps 2b, 2b+1 make Q8_0 block b; its scale d_K[cell] multiplies
+            // the block's partial product per S^T row
 #pragma unroll
-        for (int rt = 0; rt < NRT; rt++) {
-            float sv[8];
+            for (int b = 0; b < NB; b++) {
+                f32x16 cb[NH];
 #pragma unroll
-            for (int h = 0; h < 2; h++) {
-                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+                for (int c = 0; c < NH; c++)
 #pragma unroll
-                for (int ks = 0; ks < KS; ks++) {
-                    if constexpr (Q8) {
-                        // this lane's S^T rows are cells 8g + 4h + i; k-step ks = Q8_0 block ks
-                        f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[h][ks], qv[rt][ks],
-                                                                         f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[h][ks], ql[rt][ks], c, 0, 0, 0);
-                        const f32x4 dk = *(const f32x4 *) &ksc[buf][ks][8 * g + 4 * h];
+                    for (int r = 0; r < 16; r++) cb[c][r] = 0.f;
 #pragma unroll
-                        for (int i = 0; i < 4; i++) acc[i] = fmaf(c[i], dk[i], acc[i]);
-                    } else {
-                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[h][ks], qv[rt][ks], acc, 0, 0, 0);
-                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[h][ks], ql[rt][ks], acc, 0, 0, 0);
+                for (int u = 0; u < 2; u++)
+#pragma unroll
+                    for (int c = 0; c < NH; c++) {
+                        const f16x8 a = *(const f16x8 *) (Kl + 32 * c * KSTRIDE +
+                                                          tile_off<D, DMA>(n, 32 * (2 * b + u) + 16 * hh, KSTRIDE));
+                        cb[c] = mfma32(a, qv[2 * b + u], cb[c]);
+                        cb[c] = mfma32(a, ql[2 * b + u], cb[c]);
                     }
+#pragma unroll
+                for (int c = 0; c < NH; c++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const f32x4 dk = *(const f32x4 *) &ksc[buf][b][32 * c + 8 * i + 4 * hh];
+#pragma unroll
+                        for (int j = 0; j < 4; j++) sa[c][4 * i + j] = fmaf(cb[c][4 * i + j], dk[j], sa[c][4 * i + j]);
+                    }
+            }
+        } else {
+#pragma unroll
+            for (int kk = 0; kk < KK; kk++)
+#pragma unroll
+                for (int c = 0; c < NH; c++) {
+                    const f16x8 a = *(const f16x8 *) (Kl + 32 * c * KSTRIDE + tile_off<D, DMA>(n, 32 * kk + 16 * hh, KSTRIDE));
+                    sa[c] = mfma32(a, qv[kk], sa[c]);
+                    sa[c] = mfma32(a, ql[kk], sa[c]);
                 }
+            // keep four K operand reads in flight ahead of the MFMAs instead of
+            // waiting on each read right before its MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
-                for (int i = 0; i < 4; i++) sv[4 * h + i] = acc[i];
+            for (int j = 0; j < NH * KK - 4; j++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
             }
-            if (p.softcap > 0.f) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+        }
+        float sv[NS];   // scores relative to mofs
 #pragma unroll
-                for (int e = 0; e < 8; e++) sv[e] = p.softcap * tanhf(sv[e] * p.softcap_inv) * kLog2e;
+        for (int c = 0; c < NH; c++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) sv[16 * c + r] = sa[c][r];
+        if (p.softcap > 0.f) {
+#pragma unroll
+            for (int e = 0; e < NS; e++) sv[e] = p.softcap * tanhf(sv[e] * p.softcap_inv) * kLog2e;
+        }
+        if (!full) {
+#pragma unroll
+            for (int e = 0; e < NS; e++) {
+                const int r = e & 15;
+                if (cell_masked(tile + 32 * (e >> 4) + 8 * (r >> 2) + 4 * hh + (r & 3), L, prow, p.causal, p.n_swa))
+                    sv[e] = -INFINITY;
             }
-            if (!full) {
+        }
+        // Lazy rescale: the row's reference max m_run moves only when a score
+        // exceeds it by more than kRescaleSlack; the test is on the lane's own
+        // 32 cells, and the row max is formed only on the (rare, wave-uniform)
+        // tiles where some lane trips it.
+        float lmax = sv[0];
 #pragma unroll
-                for (int e = 0; e < 8; e++)
-                    if (cell_masked(tile + 8 * g + e, L, prow[rt], p.causal, p.n_swa)) sv[e] = -INFINITY;
+        for (int e = 1; e < NS; e++) lmax = fmaxf(lmax, sv[e]);
+        lmax += mofs;   // the lane's largest score
+        if (__builtin_amdgcn_ballot_w64(lmax > m_run + kRescaleSlack)) {
+            const float mt = fmaxf(lmax, __shfl_xor(lmax, 32));
+            const bool grow = mt > m_run + kRescaleSlack;
+            const float mnew = grow ? mt : m_run;
+            const float alpha = grow ? __builtin_amdgcn_exp2f(m_run - mnew) : 1.f;   // 0 from -inf
+            m_run = mnew;
+            l_run *= alpha;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const float a = __shfl(alpha, 8 * (r >> 2) + 4 * hh + (r & 3));   // alpha of O row of register r
+#pragma unroll
+                for (int m = 0; m < NO; m++) o[m][r] *= a;
             }
-            // Lazy rescale: the row's reference max m_run moves only when a
-            // score exceeds it by more than kRescaleSlack; the test is on the
-            // lane's own 8 cells, and the row-wide max is formed only on the
-            // (rare, wave-uniform) tiles where some lane trips it.
-            float lmax = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
-                               fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
-            if (__builtin_amdgcn_ballot_w64(lmax > m_run[rt] + kRescaleSlack)) {
-                const float mt = wave_max(lmax);
-                const bool grow = mt > m_run[rt] + kRescaleSlack;
-                const float mnew = grow ? mt : m_run[rt];
-                const float alpha = grow ? __builtin_amdgcn_exp2f(m_run[rt] - mnew) : 1.f;   // 0 from -inf
-                m_run[rt] = mnew;
-                l_run[rt] *= alpha;
+        }
+        // exp2 argument = score - m_run = sv + (mofs - m_run): no correction on
+        // a tile whose accumulators started at the current reference max.  A
+        // row with m_run = -inf has only masked cells so far (sv = -inf): P = 0.
+        const float delta = m_run == -INFINITY ? 0.f : mofs - m_run;
+        if (__builtin_amdgcn_ballot_w64(delta != 0.f)) {
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const float a = __shfl(alpha, 4 * g + i);   // alpha of O row 4g+i
+            for (int e = 0; e < NS; e++) sv[e] += delta;
+        }
+        // The row sum accumulates the f16 P the PV MFMA consumes (lane-partial;
+        // the two lane halves are added at the end).  Each f16 pair is its own
+        // value: hipcc (ROCm 7.2) fed v_dot2c the first dword four times when
+        // the pairs were taken as elements of a packed u32x4.
+        typedef _Float16 f16x2v __attribute__((ext_vector_type(2)));
+        const f16x2v one2 = {(_Float16) 1.0f, (_Float16) 1.0f};
+        f16x8 pa[2 * NH];   // PV step 2c + a: registers 8a .. 8a+7 of half c = cells 32c + 16a + 4hh + {0..3, 8..11}
 #pragma unroll
-                    for (int m = 0; m < NPV; m++) o[rt][m][i] *= a;
-                }
-            }
-            // a row with m_run = -inf has only masked cells so far: its P is 0
-            const float mref = m_run[rt] == -INFINITY ? 0.f : m_run[rt];
-            // The row sum accumulates the f16 P the PV MFMA consumes (lane-partial;
-            // reduced over the lane groups at the end).  Each f16 pair is its own
-            // value: hipcc (ROCm 7.2) fed v_dot2c the first dword four times when
-            // the pairs were taken as elements of the packed u32x4.
-            typedef _Float16 f16x2v __attribute__((ext_vector_type(2)));
-            const f16x2v one2 = {(_Float16) 1.0f, (_Float16) 1.0f};
+        for (int st = 0; st < 2 * NH; st++) {
             u32x4 pk;
 #pragma unroll
             for (int wi = 0; wi < 4; wi++) {
-                const f16x2v h2 = {(_Float16) __builtin_amdgcn_exp2f(sv[2 * wi] - mref),
-                                   (_Float16) __builtin_amdgcn_exp2f(sv[2 * wi + 1] - mref)};
-                l_run[rt] = __builtin_amdgcn_fdot2(h2, one2, l_run[rt], false);
+                const f16x2v h2 = {(_Float16) __builtin_amdgcn_exp2f(sv[8 * st + 2 * wi]),
+                                   (_Float16) __builtin_amdgcn_exp2f(sv[8 * st + 2 * wi + 1])};
+                l_run = __builtin_amdgcn_fdot2(h2, one2, l_run, false);
                 pk[wi] = __builtin_bit_cast(uint32_t, h2);
             }
-            pa[rt] = __builtin_bit_cast(f16x8, pk);
+            pa[st] = __builtin_bit_cast(f16x8, pk);
         }
-        const char *vrow = Vl + (4 * g + (n >> 2)) * VSTRIDE + 8 * (n & 3);
+        // V^T B operand of PV step st, output tile m: lane group l/16 reads rows
+        // 16st + 4hh + i/4 (then + 8) at dims 32m + 16((l/16)%2) + 4(i%4) and
+        // receives dim 32m + l%32 of the 4 cells
+        const int gi = lane & 15, vr = 4 * hh + (gi >> 2), vb0 = (16 * ((lane >> 4) & 1) + 4 * (gi & 3)) * 2;
 #pragma unroll
-        for (int m = 0; m < NPV; m++) {
-            const f16x8 vb = lds_tr_b16x8(vrow + 32 * m, vrow + 16 * VSTRIDE + 32 * m);
+        for (int st = 0; st < 2 * NH; st++)
 #pragma unroll
-            for (int rt = 0; rt < NRT; rt++) o[rt][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[rt], vb, o[rt][m], 0, 0, 0);
+            for (int m = 0; m < NO; m++) {
+                const char *v0 = Vl + 16 * st * VSTRIDE;
+                const f16x8 vb = lds_tr_b16x8(v0 + tile_off<D, DMA>(vr, 64 * m + vb0, VSTRIDE),
+                                              v0 + tile_off<D, DMA>(vr + 8, 64 * m + vb0, VSTRIDE));
+                o[m] = mfma32(pa[st], vb, o[m]);
+            }
+        // V transpose reads run three MFMAs ahead of their use
+        __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+#pragma unroll
+        for (int j = 0; j < 2 * NH * NO - 3; j++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
         }
+        __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
     };
 
     if (c_lo < c_hi) {
         int buf = 0;
-        load_global(c_lo);
-        store_lds(0);
-        __syncthreads();
-        for (int tile = c_lo; tile < c_hi; tile += kTile) {
-            const bool has_next = tile + kTile < c_hi;
-            if (has_next) load_global(tile + kTile);
-            compute(tile, buf);
-            if (has_next) store_lds(buf ^ 1);
+        if constexpr (DMA) {
+            // tile t + 64 streams into the other buffer while tile t is computed;
+            // one barrier per tile: every wave's loads of tile t have landed and
+            // every wave is done with the buffer the next loads overwrite
+            load_dma(c_lo, lds_k0, lds_v0);
+            for (int tile = c_lo; tile < c_hi; tile += PT) {
+                __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this wave's loads of tile t
+                __syncthreads();
+                if (tile + PT < c_hi) load_dma(tile + PT, buf ? lds_k0 : lds_k1, buf ? lds_v0 : lds_v1);
+                compute(tile, buf, buf ? lds_k1 : lds_k0, buf ? lds_v1 : lds_v0);
+                buf ^= 1;
+            }
+        } else {
+            load_global(c_lo);
+            store_lds(0);
             __syncthreads();
-            buf ^= 1;
+            for (int tile = c_lo; tile < c_hi; tile += PT) {
+                const bool has_next = tile + PT < c_hi;
+                if (has_next) load_global(tile + PT);
+                compute(tile, buf, buf ? lds_k1 : lds_k0, buf ? lds_v1 : lds_v0);
+                if (has_next) store_lds(buf ^ 1);
+                __syncthreads();
+                buf ^= 1;
+            }
         }
     }
 
     if (!wave_live) return;
+    const float lt = l_run + __shfl_xor(l_run, 32);   // row sum of query row n
 #pragma unroll
-    for (int rt = 0; rt < NRT; rt++) {
-        float l = l_run[rt];
-        l += __shfl_xor(l, 16);
-        l += __shfl_xor(l, 32);
+    for (int r = 0; r < 16; r++) {
+        const int rr = 8 * (r >> 2) + 4 * hh + (r & 3);   // row of register r
+        const float lr = __shfl(lt, rr);
+        const int row = Rw + rr;
+        if (row < M) {
+            const int t = q0 + row / p.gqa, h = hk * p.gqa + row % p.gqa;
+            const float inv = lr > 0.f ? 1.f / lr : 0.f;
+            float *op = p.out + ((int64_t) t * p.H + h) * D + n;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int r = Rw + rt * 16 + 4 * g + i;
-            const float lr = __shfl(l, 4 * g + i);
-            if (r < M) {
-                const int t = q0 + r / p.gqa, h = hk * p.gqa + r % p.gqa;
-                const float inv = lr > 0.f ? 1.f / lr : 0.f;
-                float *op = p.out + ((int64_t) t * p.H + h) * D + n;
-#pragma unroll
-                for (int m = 0; m < NPV; m++) op[16 * m] = o[rt][m][i] * inv;
-            }
+            for (int m = 0; m < NO; m++) op[32 * m] = o[m][r] * inv;
         }
     }
 }
 
-template <int D, int NRT, int NW, int KVT>
+template <int D, int NW, int KVT>
 static hipError_t launch_prefill_t(const AttnParams &p, int max_rows, hipStream_t stream) {
-    constexpr int ROWS = NW * NRT * 16;
+    constexpr int ROWS = NW * 32;
     const int n_rb = (max_rows + ROWS - 1) / ROWS;
     const int pairs_per_xcd = (p.S * p.Hkv + 7) / 8;
-    const int nwg = 8 * pairs_per_xcd * n_rb;
-    hipLaunchKernelGGL((pa_prefill_kernel<D, NRT, NW, KVT>), dim3(nwg), dim3(NW * 64), 0, stream, p, n_rb);
+    const int64_t nwg = 8 * (int64_t) pairs_per_xcd * n_rb;
+    if (nwg > INT32_MAX) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((pa_prefill_kernel<D, NW, KVT>), dim3((unsigned) nwg), dim3(NW * 64), 0, stream, p, n_rb);
     return hipGetLastError();
 }
 
 template <int KVT>
 static hipError_t launch_prefill_kv(const AttnParams &p, int head_dim, int max_rows, hipStream_t stream) {
     switch (head_dim) {
-        case 64: return launch_prefill_t<64, 2, 4, KVT>(p, max_rows, stream);
-        case 128: return launch_prefill_t<128, 1, 8, KVT>(p, max_rows, stream);
-        case 256: return launch_prefill_t<256, 1, 8, KVT>(p, max_rows, stream);
+        case 64: return launch_prefill_t<64, 4, KVT>(p, max_rows, stream);
+        case 128: return launch_prefill_t<128, 4, KVT>(p, max_rows, stream);
         default: return hipErrorInvalidValue;
     }
 }
 
 hipError_t launch_prefill(const AttnParams &p, int head_dim, int kv_type, int max_rows, hipStream_t stream) {
+    if (head_dim == 256) return launch_prefill16(p, head_dim, kv_type, max_rows, stream);
     switch (kv_type) {
         case 1: return launch_prefill_kv<1>(p, head_dim, max_rows, stream);
         case 8: return launch_prefill_kv<8>(p, head_dim, max_rows, stream);

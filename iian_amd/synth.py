@@ -14,6 +14,7 @@ Configurations (BASELINE.json ``configs``):
   cfg3            Qwen3-8B mixed batch: 4 prefill chunks of 512 tokens over a prior
                   context P~U[1024,4096] whose first 1024 tokens (64 blocks) are shared
                   by all 4 sequences, plus 32 decode tokens with L~U[1024,4096]
+                  (cfg3_prefill: the prefill chunks alone; cfg3_p0: one chunk with no prior)
   cfg4            Llama-3-8B Q8_0 KV: 128 seqs, 4096 prior + 5 spec-verify queries
   cfg5_<l>_<k>    Gemma3-12B: H16/Hkv8/D256, 32 seqs, L~U[8192,32768]; l in
                   {local (n_swa=1024), global}; k in {decode, prefill (256-token chunk)}
@@ -55,7 +56,7 @@ class Spec:
 def spec(name: str, seed: Optional[int] = None, small: bool = False) -> Spec:
     """The named configuration.  ``small`` shrinks sequence count and context
     (same heads, head size, formats and masks) for fast CPU-checked runs."""
-    base = {"cfg1": 1, "cfg2": 2, "cfg3": 3, "cfg4": 4}.get(name, 5)
+    base = {"cfg1": 1, "cfg2": 2, "cfg3": 3, "cfg3_prefill": 3, "cfg4": 4}.get(name, 5)
     rng = np.random.default_rng(seed if seed is not None else base)
     sd = seed if seed is not None else base
     if name == "cfg1":
@@ -69,6 +70,8 @@ def spec(name: str, seed: Optional[int] = None, small: bool = False) -> Spec:
         return Spec(name, 32, 8, 128, L, np.ones(S, np.int64), 65536 if not small else 4096, seed=sd)
     if name.startswith("cfg3"):
         n_pre, chunk, n_dec = (2, 64, 4) if small else (4, 512, 32)
+        if name == "cfg3_prefill":  # the prefill chunks alone (the prefill kernel without the decode rows)
+            n_dec = 0
         p_lo, p_hi = (128, 256) if small else (1024, 4096)
         P = rng.integers(p_lo, p_hi + 1, n_pre)
         if name == "cfg3_p0":       # a prefill chunk with no prior context
