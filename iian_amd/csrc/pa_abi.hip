@@ -217,9 +217,16 @@ int iian_pa_attention(void *stream, const float *q, const void *k_pool, const vo
     if (max_rows <= p.decode_rows)
         return launch_decode(p, head_dim, type_k, st) == hipSuccess ? IIAN_PA_OK : IIAN_PA_ERR_HIP;
 
-    // Mixed batch: the decode rows (HBM-bound) run on a side stream forked from
-    // and joined back into the caller's stream, beside the MFMA-bound prefill
-    // kernel, which fills the CUs first and leaves its tail to the decode waves.
+    // Mixed batch over an f16 pool (head size 64 or 128): one launch holds the
+    // prefill workgroups and, after them, the decode rows' stream-K workers,
+    // which fill the CUs the MFMA-bound prefill leaves; the merge follows.
+    if (type_k == IIAN_PA_TYPE_F16 && head_dim <= 128)
+        return launch_mixed_f16(p, head_dim, max_rows, st) == hipSuccess ? IIAN_PA_OK : IIAN_PA_ERR_HIP;
+
+    // Other mixed batches: the decode rows (HBM-bound) run on a side stream
+    // forked from and joined back into the caller's stream, beside the
+    // MFMA-bound prefill kernel, which fills the CUs first and leaves its tail
+    // to the decode waves.
     const SideStream *side = side_stream_for(st);
     if (!side) return IIAN_PA_ERR_HIP;
     if (hipEventRecord(side->fork, st) != hipSuccess || hipStreamWaitEvent(side->stream, side->fork, 0) != hipSuccess)

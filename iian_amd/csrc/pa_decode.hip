@@ -31,260 +31,9 @@
 // (:124), softcap (:127), all-masked rows -> 0 (:132).
 #include "pa_common.h"
 #include "pa_launch.h"
+#include "pa_decode_body.h"
 
 namespace iian_pa {
-
-// K/V are read once per call: non-temporal loads keep them from evicting the
-// block tables and partials.  Measured on MI355X: +5% at D=128 (256-byte head
-// slices), -7% at D=256, so it is chosen per head size.
-template <int D>
-struct KvStream {
-    static constexpr bool kNonTemporal = D <= 128;
-};
-
-template <int D, typename T>
-__device__ __forceinline__ T stream_load(const T *ptr) {
-    if constexpr (KvStream<D>::kNonTemporal)
-        return __builtin_nontemporal_load(ptr);
-    else
-        return *ptr;
-}
-
-template <int D>
-struct KRegs {
-    u32x4 k[2][D / 32];
-};
-template <int D>
-struct VRegs {
-    uint32_t v[8][D / 32];   // 8 cells x (D/16) halves per lane
-};
-
-// K: lane (n, g) loads cells tile + 8*(n/4) + 4h + (n%4), dims 32ks + 8g .. +8
-template <int D>
-__device__ __forceinline__ void load_k(const AttnParams &p, const TableWindow &tw, int L, int hk, int tile,
-                                       KRegs<D> &r) {
-    const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
-    const int last = L - 1;
-    const int grp = min(tile + 8 * (n >> 2), last);
-#pragma unroll
-    for (int h = 0; h < 2; h++) {
-        const int c = min(tile + 8 * (n >> 2) + 4 * h + (n & 3), last);
-        const int64_t row = table_row(p, tw, grp, c);
-        const char *base = p.k_pool + row * p.k_row + (int64_t) hk * D * 2 + g * 16;
-#pragma unroll
-        for (int ks = 0; ks < D / 32; ks++) r.k[h][ks] = stream_load<D>((const u32x4 *) (base + ks * 64));
-    }
-}
-
-// V: lane (n, g) loads cells tile + 8g + e, dims (D/16)*n .. +D/16
-template <int D>
-__device__ __forceinline__ void load_v(const AttnParams &p, const TableWindow &tw, int L, int hk, int tile,
-                                       VRegs<D> &r) {
-    constexpr int VW = D / 32;
-    const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
-    const int last = L - 1;
-    const int grp = min(tile + 8 * g, last);
-#pragma unroll
-    for (int e = 0; e < 8; e++) {
-        const int c = min(tile + 8 * g + e, last);
-        const int64_t row = table_row(p, tw, grp, c);
-        const uint32_t *src = (const uint32_t *) (p.v_pool + row * p.v_row + (int64_t) hk * D * 2 + n * (D / 8));
-        if constexpr (VW == 2) {
-            const u32x2 x = stream_load<D>((const u32x2 *) src);
-            r.v[e][0] = x[0];
-            r.v[e][1] = x[1];
-        } else {
-#pragma unroll
-            for (int i = 0; i < VW; i += 4) {
-                const u32x4 x = stream_load<D>((const u32x4 *) (src + i));
-                r.v[e][i] = x[0];
-                r.v[e][i + 1] = x[1];
-                r.v[e][i + 2] = x[2];
-                r.v[e][i + 3] = x[3];
-            }
-        }
-    }
-}
-
-// One piece: window tiles [pc.t0, pc.t1) of sequence pc.s at kv head pc.hk.
-template <int D, int NRT>
-__device__ __forceinline__ void decode_piece(const AttnParams &p, const SeqWindow &w, const Piece &pc) {
-    constexpr int KS = D / 32;
-    constexpr int DPL = D / 16;
-    const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
-    const int s = pc.s, hk = pc.hk;
-    const int M = w.nq * p.gqa;
-    const int cb = w.c_lo + pc.t0 * kTile;
-    const int ce = min(w.c_hi, w.c_lo + pc.t1 * kTile);
-
-    TableWindow tw;
-    if (cb < ce) table_load(p, s, cb >> p.bs_log2, w.L, tw);
-
-    // Q^T B operands (pre-scaled f16 hi/lo pairs), row positions, running state
-    f16x8 qh[NRT][KS], ql[NRT][KS];
-    int prow[NRT];
-    float m_run[NRT], l_run[NRT];
-    f32x4 o[NRT][DPL];
-#pragma unroll
-    for (int rt = 0; rt < NRT; rt++) {
-        const int r = rt * 16 + n;
-        prow[rt] = w.pmax;
-        if (r < M) {
-            const int t = w.q0 + r / p.gqa, h = hk * p.gqa + r % p.gqa;
-            prow[rt] = p.pos[t];
-            const float *qp = p.q + ((int64_t) t * p.H + h) * D + 8 * g;
-#pragma unroll
-            for (int ks = 0; ks < KS; ks++)
-                split_f16x8(*(const float4 *) (qp + 32 * ks), *(const float4 *) (qp + 32 * ks + 4), p.qscale,
-                            qh[rt][ks], ql[rt][ks]);
-        } else {
-#pragma unroll
-            for (int ks = 0; ks < KS; ks++)
-                qh[rt][ks] = ql[rt][ks] = __builtin_bit_cast(f16x8, u32x4{0u, 0u, 0u, 0u});
-        }
-        m_run[rt] = -INFINITY;
-        l_run[rt] = 0.f;
-#pragma unroll
-        for (int m = 0; m < DPL; m++) o[rt][m] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-
-    if (cb < ce) {
-        KRegs<D> kr;
-        VRegs<D> vr;
-        load_k<D>(p, tw, w.L, hk, cb, kr);
-        load_v<D>(p, tw, w.L, hk, cb, vr);
-        for (int tile = cb; tile < ce; tile += kTile) {
-            const int next = tile + kTile;
-            const bool has_next = next < ce;
-            if (has_next && ((min(next + kTile - 1, w.L - 1) >> p.bs_log2) - tw.first) >= 64)
-                table_load(p, s, next >> p.bs_log2, w.L, tw);   // pieces longer than 64 blocks
-
-            // S^T = K Q^T for every row tile
-            f32x4 sacc[NRT][2];
-#pragma unroll
-            for (int rt = 0; rt < NRT; rt++)
-#pragma unroll
-                for (int h = 0; h < 2; h++) {
-                    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                    for (int ks = 0; ks < KS; ks++) {
-                        const f16x8 a = __builtin_bit_cast(f16x8, kr.k[h][ks]);
-                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qh[rt][ks], acc, 0, 0, 0);
-                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ql[rt][ks], acc, 0, 0, 0);
-                    }
-                    sacc[rt][h] = acc;
-                }
-            if (has_next) load_k<D>(p, tw, w.L, hk, next, kr);
-
-            // online softmax; P becomes the A operand of PV
-            const bool full = tile + kTile <= w.L && (!p.causal || tile + kTile - 1 <= w.pmin) &&
-                              (p.n_swa <= 0 || w.pmax - tile < p.n_swa);
-            f16x8 pa[NRT];
-#pragma unroll
-            for (int rt = 0; rt < NRT; rt++) {
-                float sv[8];
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    sv[i] = sacc[rt][0][i];
-                    sv[4 + i] = sacc[rt][1][i];
-                }
-                if (p.softcap > 0.f) {
-#pragma unroll
-                    for (int e = 0; e < 8; e++) sv[e] = p.softcap * tanhf(sv[e] * p.softcap_inv) * kLog2e;
-                }
-                if (!full) {
-#pragma unroll
-                    for (int e = 0; e < 8; e++)
-                        if (cell_masked(tile + 8 * g + e, w.L, prow[rt], p.causal, p.n_swa)) sv[e] = -INFINITY;
-                }
-                float mt = sv[0];
-#pragma unroll
-                for (int e = 1; e < 8; e++) mt = fmaxf(mt, sv[e]);
-                mt = wave_max(mt);
-                const float mnew = fmaxf(m_run[rt], mt);
-                float alpha = 1.f;
-                float pv[8];
-                if (mnew == -INFINITY) {
-#pragma unroll
-                    for (int e = 0; e < 8; e++) pv[e] = 0.f;
-                } else {
-                    alpha = __builtin_amdgcn_exp2f(m_run[rt] - mnew);
-#pragma unroll
-                    for (int e = 0; e < 8; e++) pv[e] = __builtin_amdgcn_exp2f(sv[e] - mnew);
-                }
-                m_run[rt] = mnew;
-                float ps = 0.f;
-#pragma unroll
-                for (int e = 0; e < 8; e++) ps += pv[e];
-                l_run[rt] = l_run[rt] * alpha + ps;
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const float a = __shfl(alpha, 4 * g + i);   // alpha of O row 4g+i
-#pragma unroll
-                    for (int m = 0; m < DPL; m++) o[rt][m][i] *= a;
-                }
-                u32x4 pk;
-#pragma unroll
-                for (int wi = 0; wi < 4; wi++) pk[wi] = pack_f16x2(pv[2 * wi], pv[2 * wi + 1]);
-                pa[rt] = __builtin_bit_cast(f16x8, pk);
-            }
-
-            // V^T B operands: MFMA m takes dim DPL*n + m of cells 8g .. 8g+7
-            u32x4 vb[DPL];
-#pragma unroll
-            for (int m = 0; m < DPL; m++) {
-                const uint32_t sel = (m & 1) ? 0x07060302u : 0x05040100u;
-#pragma unroll
-                for (int wi = 0; wi < 4; wi++)
-                    vb[m][wi] = __builtin_amdgcn_perm(vr.v[2 * wi + 1][m >> 1], vr.v[2 * wi][m >> 1], sel);
-            }
-            if (has_next) load_v<D>(p, tw, w.L, hk, next, vr);
-#pragma unroll
-            for (int m = 0; m < DPL; m++)
-#pragma unroll
-                for (int rt = 0; rt < NRT; rt++)
-                    o[rt][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[rt], __builtin_bit_cast(f16x8, vb[m]),
-                                                                      o[rt][m], 0, 0, 0);
-        }
-    }
-
-    if (pc.t0 == 0 && lane == 0) p.seg_info[pc.seg] = make_int2(pc.rec, pc.pieces);
-#pragma unroll
-    for (int rt = 0; rt < NRT; rt++) {
-        float l = l_run[rt];
-        l += __shfl_xor(l, 16);
-        l += __shfl_xor(l, 32);
-        if (pc.pieces == 1) {
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int r = rt * 16 + 4 * g + i;
-                const float lr = __shfl(l, 4 * g + i);
-                if (r < M) {
-                    const int t = w.q0 + r / p.gqa, h = hk * p.gqa + r % p.gqa;
-                    const float inv = lr > 0.f ? 1.f / lr : 0.f;
-                    float *op = p.out + ((int64_t) t * p.H + h) * D + DPL * n;
-#pragma unroll
-                    for (int m = 0; m < DPL; m += 4)
-                        *(float4 *) (op + m) = make_float4(o[rt][m][i] * inv, o[rt][m + 1][i] * inv,
-                                                           o[rt][m + 2][i] * inv, o[rt][m + 3][i] * inv);
-                }
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int r = rt * 16 + 4 * g + i;
-                if (r < M) {
-                    float *op = rec_o(p, pc.rec, 0, r, D) + DPL * n;
-#pragma unroll
-                    for (int m = 0; m < DPL; m += 4)
-                        *(float4 *) (op + m) = make_float4(o[rt][m][i], o[rt][m + 1][i], o[rt][m + 2][i], o[rt][m + 3][i]);
-                }
-            }
-            const int r = rt * 16 + n;
-            if (g == 0 && r < M) *(float2 *) rec_ml(p, pc.rec, 0, r) = make_float2(m_run[rt], l);
-        }
-    }
-}
 
 // One wave per SIMD is launched (kF16DecodeWaves in pa_abi.hip), but the
 // register budget stays at two waves per SIMD up to D*NRT = 128: in a mixed

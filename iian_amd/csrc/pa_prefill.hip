@@ -34,6 +34,7 @@
 #include "pa_common.h"
 #include "pa_launch.h"
 #include "pa_mfma.h"
+#include "pa_decode_body.h"
 
 namespace iian_pa {
 
@@ -50,8 +51,27 @@ struct PrefillOcc {
 // values in f16 plus the block scales d as f32 in LDS, applied per cell after
 // the two QK^T k-steps of each block, so q*d enters the scores exactly; V as
 // f16(q*d), the correctly rounded dequantised value.
-template <int D, int NW, int KVT>
-__global__ __launch_bounds__(NW * 64, PrefillOcc<D>::kWavesPerSimd) void pa_prefill_kernel(AttnParams p, int n_rb) {
+//
+// MIXED: the launch of a mixed batch over an f16 pool.  The first n_dec
+// workgroups hold NW stream-K decode workers each (one wave per worker,
+// decode_piece of pa_decode_body.h) and are dispatched first, one per CU: the
+// HBM-bound decode waves and the MFMA-bound prefill workgroups then share
+// every CU from the start, instead of the decode rows waiting for the prefill
+// tail.  The merge kernel follows on the same stream.
+template <int D, int NW, int KVT, bool MIXED>
+__global__ __launch_bounds__(NW * 64, PrefillOcc<D>::kWavesPerSimd) void pa_prefill_kernel(AttnParams p, int n_rb,
+                                                                                          int n_dec) {
+    int bid = blockIdx.x;
+    if constexpr (MIXED) {
+        if (bid < n_dec) {
+            const int worker = bid * NW + (int) (threadIdx.x >> 6);
+            if (worker < p.sk_workers)
+                for_each_piece<false>(p, worker, 0,
+                                      [&](const SeqWindow &w, const Piece &pc) { decode_piece<D, 1>(p, w, pc); });
+            return;
+        }
+        bid -= n_dec;   // a multiple of 8: the XCD of every prefill workgroup is unchanged
+    }
     constexpr bool DMA = KVT == 1 && D >= 128;   // f16 tiles loaded straight into LDS
     using SH = PrefillShape<D, DMA>;
     constexpr int KK = SH::KK, NO = SH::NO, KSTRIDE = SH::KSTRIDE, VSTRIDE = SH::VSTRIDE;
@@ -76,7 +96,6 @@ __global__ __launch_bounds__(NW * 64, PrefillOcc<D>::kWavesPerSimd) void pa_pref
     // all row blocks of a pair run on its XCD, so they share K/V through that
     // XCD's L2, while neighbouring pairs (the ones that carry work when only a
     // few sequences of a batch are prefill chunks) land on different XCDs.
-    const int bid = blockIdx.x;
     const int slot = bid >> 3;
     const int pair = (bid & 7) + 8 * (slot / n_rb);
     const int rb = slot % n_rb;
@@ -456,24 +475,37 @@ __global__ __launch_bounds__(NW * 64, PrefillOcc<D>::kWavesPerSimd) void pa_pref
     }
 }
 
-template <int D, int NW, int KVT>
+template <int D, int NW, int KVT, bool MIXED>
 static hipError_t launch_prefill_t(const AttnParams &p, int max_rows, hipStream_t stream) {
     constexpr int ROWS = NW * 32;
     const int n_rb = (max_rows + ROWS - 1) / ROWS;
     const int pairs_per_xcd = (p.S * p.Hkv + 7) / 8;
-    const int64_t nwg = 8 * (int64_t) pairs_per_xcd * n_rb;
+    const int64_t n_pf = 8 * (int64_t) pairs_per_xcd * n_rb;
+    const int64_t n_dec = MIXED ? ((p.sk_workers + NW - 1) / NW + 7) / 8 * 8 : 0;
+    const int64_t nwg = n_dec + n_pf;
     if (nwg > INT32_MAX) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((pa_prefill_kernel<D, NW, KVT>), dim3((unsigned) nwg), dim3(NW * 64), 0, stream, p, n_rb);
+    hipLaunchKernelGGL((pa_prefill_kernel<D, NW, KVT, MIXED>), dim3((unsigned) nwg), dim3(NW * 64), 0, stream, p, n_rb,
+                       (int) n_dec);
     return hipGetLastError();
 }
 
 template <int KVT>
 static hipError_t launch_prefill_kv(const AttnParams &p, int head_dim, int max_rows, hipStream_t stream) {
     switch (head_dim) {
-        case 64: return launch_prefill_t<64, 4, KVT>(p, max_rows, stream);
-        case 128: return launch_prefill_t<128, 4, KVT>(p, max_rows, stream);
+        case 64: return launch_prefill_t<64, 4, KVT, false>(p, max_rows, stream);
+        case 128: return launch_prefill_t<128, 4, KVT, false>(p, max_rows, stream);
         default: return hipErrorInvalidValue;
     }
+}
+
+hipError_t launch_mixed_f16(const AttnParams &p, int head_dim, int max_rows, hipStream_t stream) {
+    hipError_t e;
+    switch (head_dim) {
+        case 64: e = launch_prefill_t<64, 4, 1, true>(p, max_rows, stream); break;
+        case 128: e = launch_prefill_t<128, 4, 1, true>(p, max_rows, stream); break;
+        default: return hipErrorInvalidValue;
+    }
+    return e != hipSuccess ? e : launch_merge(p, head_dim, stream);
 }
 
 hipError_t launch_prefill(const AttnParams &p, int head_dim, int kv_type, int max_rows, hipStream_t stream) {
