@@ -56,13 +56,33 @@ def pmc_traffic(config: str):
     return None if rec is None else int(rec["traffic_bytes_per_launch"])
 
 
+def launch_kernels(sp, pa) -> str:
+    """The kernels one iian_pa_attention call of this workload launches."""
+    gqa = sp.H // sp.Hkv
+    rows = [int(n) * gqa for n in sp.n_q]
+    has_dec = any(0 < r <= 32 for r in rows)
+    has_pf = any(r > 32 for r in rows)
+    d = sp.D
+    if sp.kv_type == pa.GGML_TYPE_Q8_0:
+        dec = f"pa_decode_q8_kernel<{d}> + pa_merge_kernel<{d}>"
+        pf = f"pa_prefill_kernel<{d}, Q8_0>" if d <= 128 else f"pa_prefill16_kernel<{d}, Q8_0>"
+    else:
+        dec = f"pa_decode_f16_kernel<{d}> + pa_merge_kernel<{d}>"
+        pf = f"pa_prefill_kernel<{d}, f16>" if d <= 128 else f"pa_prefill16_kernel<{d}, f16>"
+        if has_dec and has_pf and d <= 128:
+            return f"pa_prefill_kernel<{d}, f16, mixed> (decode pieces in the same grid) + pa_merge_kernel<{d}>"
+    if has_dec and has_pf:
+        return f"{pf} || {dec} (two streams)"
+    return pf if has_pf else dec
+
+
 def cpu_baseline(w, runs: int = 5):
     """Median wall time of the CPU oracle over the same step (KV write + all
     (token, head) items), using every host core."""
     import numpy as np
     from oracle import oracle
     sp = w.spec
-    threads = os.cpu_count() or 1
+    threads = min(os.cpu_count() or 1, 16)   # the host-core share of one GPU
     kp = w.k_pool.data.cpu().numpy()
     vp = w.v_pool.data.cpu().numpy()
     q = w.q.cpu().numpy()
@@ -115,8 +135,7 @@ def main() -> int:
     stream = torch.cuda.current_stream()
 
     def kv_write():
-        pa.set_rows(w.k_pool, w.k_new, w.batch.slots)
-        pa.set_rows(w.v_pool, w.v_new, w.batch.slots)
+        pa.set_rows_kv(w.k_pool, w.v_pool, w.k_new, w.v_new, w.batch.slots)
 
     def attention():
         pa.build_paged_attn(w.q, w.k_pool, w.v_pool, sp.Hkv, w.params, w.batch, out=out, workspace=ws)
@@ -194,9 +213,7 @@ def main() -> int:
         "attn_tok_per_s": round(w.T / (attn_ms * 1e-3), 1),
         "roofline": {
             "bound": "mfma" if mfma_bound else "hbm",
-            "kernel": "iian_pa_attention (" + ("pa_prefill_kernel" if mfma_bound else
-                                               ("pa_decode_q8_kernel" if sp.kv_type == pa.GGML_TYPE_Q8_0
-                                                else "pa_decode_f16_kernel") + " + pa_merge_kernel") + ")",
+            "kernel": "iian_pa_attention (" + launch_kernels(sp, pa) + ")",
             "achieved": round(attn_tfs if mfma_bound else attn_gbs, 1),
             "peak": MFMA_F16_PEAK_TFLOPS if mfma_bound else HBM_PEAK_GBS,
             "unit": "TFLOP/s" if mfma_bound else "GB/s",

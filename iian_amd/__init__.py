@@ -18,6 +18,7 @@ from .paged_attn import (  # noqa: F401
     paged_attn_supported,
     row_bytes,
     set_rows,
+    set_rows_kv,
     workspace_size,
 )
 from ._lib import PagedAttnError  # noqa: F401

@@ -29,6 +29,7 @@ SIGNATURES = {
     "iian_pa_status_string": (C.c_char_p, [C.c_int]),
     "iian_pa_supported": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_float]),
     "iian_pa_kv_write": (C.c_int, [_P, _P, _I64, _I64, _P, _P, _I64, C.c_int, _P]),
+    "iian_pa_kv_write_kv": (C.c_int, [_P, _P, _P, _I64, _I64, _I64, _P, _P, _P, _I64, C.c_int, C.c_int, _P]),
     "iian_pa_workspace_size": (C.c_size_t, [_I32, _I32, _I32, _I32, _I32, _I32, _I32]),
     "iian_pa_attention": (C.c_int, [_P, _P, _P, _P, C.c_int, C.c_int, _I32, _P, _I32, _P, _P, _P,
                                     _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32,

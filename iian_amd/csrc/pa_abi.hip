@@ -136,6 +136,22 @@ int iian_pa_kv_write(void *stream, const float *rows, int64_t n_rows, int64_t ro
     return e == hipSuccess ? IIAN_PA_OK : IIAN_PA_ERR_HIP;
 }
 
+int iian_pa_kv_write_kv(void *stream, const float *k_rows, const float *v_rows, int64_t n_rows,
+                        int64_t k_row_elems, int64_t v_row_elems, const int64_t *slots, void *k_pool, void *v_pool,
+                        int64_t n_cells, int type_k, int type_v, int32_t *err_flag) {
+    if (n_rows < 0 || k_row_elems <= 0 || v_row_elems <= 0 || n_cells < 0) return IIAN_PA_ERR_ARG;
+    if (n_rows == 0) return IIAN_PA_OK;
+    if (!k_rows || !v_rows || !slots || !k_pool || !v_pool) return IIAN_PA_ERR_NULL;
+    int64_t kb, vb;
+    int rc = row_bytes(type_k, k_row_elems, kb);
+    if (rc) return rc;
+    rc = row_bytes(type_v, v_row_elems, vb);
+    if (rc) return rc;
+    const hipError_t e = launch_kv_write_kv(k_rows, v_rows, n_rows, k_row_elems, v_row_elems, slots, k_pool, v_pool,
+                                            n_cells, type_k, type_v, err_flag, (hipStream_t) stream);
+    return e == hipSuccess ? IIAN_PA_OK : IIAN_PA_ERR_HIP;
+}
+
 size_t iian_pa_workspace_size(int32_t n_tokens, int32_t n_seqs, int32_t n_head, int32_t n_head_kv,
                               int32_t head_dim_v, int32_t max_blocks, int32_t block_size) {
     if (n_tokens < 0 || n_seqs < 0 || n_head <= 0 || n_head_kv <= 0 || head_dim_v <= 0 || max_blocks < 0 ||

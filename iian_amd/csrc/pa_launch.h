@@ -21,6 +21,10 @@ hipError_t launch_prefill16(const AttnParams &p, int head_dim, int kv_type, int 
 
 hipError_t launch_kv_write(const float *rows, int64_t n_rows, int64_t row_elems, const int64_t *slots, void *pool,
                            int64_t n_cells, int type, int32_t *err, hipStream_t stream);
+// K and V pools of one layer over one slot list: one launch when the types match.
+hipError_t launch_kv_write_kv(const float *k_rows, const float *v_rows, int64_t n_rows, int64_t k_row_elems,
+                              int64_t v_row_elems, const int64_t *slots, void *k_pool, void *v_pool, int64_t n_cells,
+                              int type_k, int type_v, int32_t *err, hipStream_t stream);
 hipError_t launch_dequant_q8_0(const void *pool, int64_t n_cells, const int64_t *rows_idx, int64_t n_rows,
                                int64_t row_elems, float *out, hipStream_t stream);
 

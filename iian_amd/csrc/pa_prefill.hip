@@ -3,8 +3,12 @@
 // One workgroup of NW waves per (row block, kv head, sequence); rows are
 // r = j*gqa + g (query token j, head g of the GQA group) and every wave owns 32
 // of them.  The workgroup streams the sequence's cells in 64-cell tiles
-// through the block table into LDS (register-staged double buffer) and every
-// wave reuses each tile for its 32 rows:
+// through the block table into a double-buffered LDS tile pair and every wave
+// reuses each tile for its 32 rows.  f16 tiles at D >= 128 go straight from
+// HBM to LDS (global_load_lds_dwordx4, rows unpadded with their 16-byte chunks
+// XOR-swizzled, issued from inline asm so that reads of the other buffer do not
+// wait on them); D = 64 and Q8_0 tiles are staged through registers (padded
+// rows).  Per tile:
 //
 //   S^T = K * Q^T       v_mfma_f32_32x32x16_f16: K rows (cells) from LDS with
 //                       ds_read_b128 as the A operand, Q^T (f16 hi/lo pair)

@@ -182,6 +182,25 @@ def set_rows(pool: KVPool, rows: torch.Tensor, slots: torch.Tensor, err_flag: Op
     return pool
 
 
+def set_rows_kv(k_pool: KVPool, v_pool: KVPool, k_rows: torch.Tensor, v_rows: torch.Tensor, slots: torch.Tensor,
+                err_flag: Optional[torch.Tensor] = None) -> None:
+    """The layer's two set_rows calls (K pool, then V pool, same slots;
+    src/iian/graph.cpp:319-320) as one launch when the pool types match."""
+    for pool, rows in ((k_pool, k_rows), (v_pool, v_rows)):
+        if rows.dtype != torch.float32 or rows.dim() != 2 or rows.shape[1] != pool.n_embd:
+            raise ValueError("rows must be f32 [n_tokens, n_embd]")
+    if k_rows.shape[0] != v_rows.shape[0] or k_pool.n_cells != v_pool.n_cells:
+        raise ValueError("K and V must have the same token count and cell count")
+    if slots.dtype != torch.int64 or slots.shape != (k_rows.shape[0],):
+        raise ValueError("slots must be int64 [n_tokens]")
+    k_rows, v_rows = k_rows.contiguous(), v_rows.contiguous()
+    lib = _lib.load()
+    st = lib.iian_pa_kv_write_kv(_stream(), k_rows.data_ptr(), v_rows.data_ptr(), k_rows.shape[0], k_rows.shape[1],
+                                 v_rows.shape[1], slots.data_ptr(), k_pool.data.data_ptr(), v_pool.data.data_ptr(),
+                                 k_pool.n_cells, k_pool.type, v_pool.type, _ptr(err_flag))
+    _lib.check("iian_pa_kv_write_kv", st)
+
+
 def workspace_size(n_tokens: int, n_seqs: int, n_head: int, n_head_kv: int, head_dim_v: int, max_blocks: int,
                    block_size: int) -> int:
     return int(_lib.load().iian_pa_workspace_size(n_tokens, n_seqs, n_head, n_head_kv, head_dim_v, max_blocks,

@@ -69,6 +69,18 @@ int iian_pa_kv_write(void *stream, const float *rows, int64_t n_rows, int64_t ro
                      const int64_t *slots, void *pool, int64_t n_cells, int type,
                      int32_t *err_flag);
 
+/* The two ggml_set_rows calls of one layer (K pool, then V pool, over the
+ * same slots: src/iian/graph.cpp:319-320) as one entry point and, when
+ * type_k == type_v, one launch:
+ *   k_pool row slots[t] <- convert(k_rows[t]),  v_pool row slots[t] <- convert(v_rows[t])
+ * k_rows: f32 [n_rows][k_row_elems]; v_rows: f32 [n_rows][v_row_elems]; both
+ * pools hold n_cells rows.  Conversions, slot rules and *err_flag as
+ * iian_pa_kv_write. */
+int iian_pa_kv_write_kv(void *stream, const float *k_rows, const float *v_rows, int64_t n_rows,
+                        int64_t k_row_elems, int64_t v_row_elems, const int64_t *slots,
+                        void *k_pool, void *v_pool, int64_t n_cells, int type_k, int type_v,
+                        int32_t *err_flag);
+
 /* Bytes of device workspace iian_pa_attention needs for these sizes (split-K
  * partial results).  Returns 0 on invalid arguments.  No counterpart in the
  * reference, whose CPU op keeps its scratch in thread_local vectors

@@ -112,6 +112,21 @@ def test_kv_write_rejects_invalid_arguments(lib):
     assert f(None, 0x1000, 0, 128, 0x2000, 0x3000, 64, 1, None) == 0       # nothing to do
 
 
+def test_kv_write_kv_rejects_invalid_arguments(lib):
+    f = lib.iian_pa_kv_write_kv
+    ok = dict(k=0x1000, v=0x1100, n=4, ek=128, ev=128, slots=0x2000, kp=0x3000, vp=0x4000, cells=64, tk=1, tv=1)
+
+    def call(**over):
+        a = dict(ok, **over)
+        return f(None, a["k"], a["v"], a["n"], a["ek"], a["ev"], a["slots"], a["kp"], a["vp"], a["cells"], a["tk"],
+                 a["tv"], None)
+    assert call(v=None) == -1 and call(vp=None) == -1 and call(slots=None) == -1
+    assert call(n=-1) == -2 and call(ev=0) == -2
+    assert call(tv=8, ev=100) == -2                                     # Q8_0 needs 32-multiples
+    assert call(tk=2) == -3
+    assert call(n=0) == 0
+
+
 def test_dequant_rejects_invalid_arguments(lib):
     f = lib.iian_pa_dequant_q8_0
     assert f(None, None, 64, 0x2000, 4, 128, 0x3000) == -1

@@ -57,6 +57,33 @@ def test_kv_write_bit_exact(pa, oracle, type_, n_embd):
     assert np.array_equal(got, want)
 
 
+@pytest.mark.parametrize("tk,tv,ek,ev", [(F16, F16, 1024, 1024), (Q8_0, Q8_0, 1024, 512), (F16, F16, 256, 100),
+                                         (F32, F32, 256, 256), (F16, Q8_0, 512, 512)])
+def test_kv_write_kv_bit_exact(pa, oracle, tk, tv, ek, ev):
+    """One call writes both pools; each must equal its own set_rows oracle
+    (rows of different lengths exercise the shared grid's tail)."""
+    banner(f"kv_write_kv types={tk},{tv} n_embd={ek},{ev}")
+    rng = np.random.default_rng(300 + tk + tv + ek + ev)
+    n_cells, T = 2048, 96
+    pools, wants, rows = [], [], []
+    for t, e in ((tk, ek), (tv, ev)):
+        init = rng.integers(0, 256, (n_cells, pa.row_bytes(t, e)), dtype=np.uint8)
+        r = rng.standard_normal((T, e)).astype(np.float32)
+        pools.append(pa.KVPool.wrap(torch.as_tensor(init).cuda(), e, t))
+        wants.append(init.copy())
+        rows.append(r)
+    slots = rng.choice(n_cells, T, replace=False).astype(np.int64)
+    slots[5] = n_cells          # out of range: skipped in both pools, flagged
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    pa.set_rows_kv(pools[0], pools[1], torch.as_tensor(rows[0]).cuda(), torch.as_tensor(rows[1]).cuda(),
+                   torch.as_tensor(slots).cuda(), err)
+    keep = np.arange(T) != 5
+    for pool, want, r, t in zip(pools, wants, rows, (tk, tv)):
+        assert oracle.set_rows(want, r[keep], slots[keep], t) == 0
+        assert np.array_equal(pool.data.cpu().numpy(), want)
+    assert int(err.item()) & 1
+
+
 def test_kv_write_out_of_range_slot_is_flagged_not_written(pa):
     banner("kv_write out-of-range slot")
     n_cells = 64
