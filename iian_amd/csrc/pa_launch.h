@@ -5,7 +5,7 @@
 
 namespace iian_pa {
 
-// Decode / spec-verify kernel (sequences with n_q*gqa <= p.decode_rows) plus the split-K merge.
+// Decode / spec-verify kernel (sequences with n_q*gqa <= p.decode_rows) plus the stream-K merge.
 hipError_t launch_decode(const AttnParams &p, int head_dim, int kv_type, hipStream_t stream);
 // The Q8_0-pool variant of launch_decode (pa_decode_q8.hip).
 hipError_t launch_decode_q8(const AttnParams &p, int head_dim, hipStream_t stream);

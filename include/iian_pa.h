@@ -81,8 +81,9 @@ int iian_pa_kv_write_kv(void *stream, const float *k_rows, const float *v_rows, 
                         void *k_pool, void *v_pool, int64_t n_cells, int type_k, int type_v,
                         int32_t *err_flag);
 
-/* Bytes of device workspace iian_pa_attention needs for these sizes (split-K
- * partial results).  Returns 0 on invalid arguments.  No counterpart in the
+/* Bytes of device workspace iian_pa_attention needs for these sizes (stream-K
+ * partial records of the decode rows; the size depends on n_seqs, n_head_kv
+ * and head_dim_v only).  Returns 0 on invalid arguments.  No counterpart in the
  * reference, whose CPU op keeps its scratch in thread_local vectors
  * (src/iian/paged_attn.cpp:108-110).  The workspace needs no initialisation and
  * can be reused by later calls on the same stream; concurrent calls (different

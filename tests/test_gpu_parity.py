@@ -141,7 +141,7 @@ def oracle_attention(oracle, c, items=None):
 SMALL = {
     # name: (H, Hkv, D, lens, nq, kwargs)            which kernel
     "decode_gqa7_d64": (14, 2, 64, [64, 200, 1000, 17, 1], [1, 1, 1, 1, 1], {}),        # decode, 1 tile
-    "decode_gqa4_d128": (32, 8, 128, [513, 77, 2048, 33], [1, 1, 1, 1], {}),            # decode + split-K merge
+    "decode_gqa4_d128": (32, 8, 128, [513, 77, 2048, 33], [1, 1, 1, 1], {}),            # decode + stream-K merge
     "decode_gqa2_d256": (16, 8, 256, [1500, 40], [1, 1], {}),
     "decode_long_splits": (8, 2, 128, [9000, 5000], [1, 1], {}),                        # 18 splits
     "spec_verify_5": (32, 8, 128, [700, 101, 4101], [5, 5, 5], {}),                     # decode, 2 row tiles
