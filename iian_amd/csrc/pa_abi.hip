@@ -21,8 +21,12 @@ using namespace iian_pa;
 // prefetch gains nothing, so the pool's access pattern, not the number of
 // loads in flight, sets the rate.  The Q8_0 kernel's workers are groups of Hkv
 // workgroups of NW waves over 2048 waves: its LDS staging and conversion want
-// two waves per SIMD (1024 waves measured 1.7x slower at config 4).
+// two waves per SIMD (1024 waves measured 1.7x slower at config 4).  At head
+// size 256 a tile moves twice the bytes and 768 waves measured best (Gemma3-12B
+// shapes: sliding-window layer 50.6 us against 56.6 us at 1024, 58.0 at 640,
+// 60.9 at 512, 61.1 at 2048; global layer 808 us against 824 us at 1024).
 constexpr int kF16DecodeWaves = 1024;
+constexpr int kF16DecodeWavesD256 = 768;
 constexpr int kQ8DecodeWaves = 2048;
 constexpr int kDecodeWaves = kQ8DecodeWaves > kF16DecodeWaves ? kQ8DecodeWaves : kF16DecodeWaves;
 
@@ -221,7 +225,7 @@ int iian_pa_attention(void *stream, const float *q, const void *k_pool, const vo
         p.sk_workers = std::max(1, kQ8DecodeWaves / (q8_waves_per_wg(p.decode_rows) * n_head_kv));
     } else {
         p.rec_heads = 1;
-        p.sk_workers = kF16DecodeWaves;
+        p.sk_workers = head_dim == 256 ? kF16DecodeWavesD256 : kF16DecodeWaves;
     }
     p.rec_stride = (int64_t) p.rec_heads * p.decode_rows * head_dim_v + kRecordPad;
     const WorkspaceLayout wl = workspace_layout(n_seqs, n_head_kv, head_dim_v);

@@ -326,6 +326,12 @@ __global__ __launch_bounds__(NW * 64, PrefillOcc<D>::kWavesPerSimd) void pa_pref
                     }
             }
         } else {
+            // Issue priority up for the MFMA clusters (QK^T here, PV below):
+            // of the two waves on a SIMD, the one with MFMAs to issue goes
+            // first and the other's softmax VALU fills the MFMA shadow, instead
+            // of both waves reaching their softmax at the same time (measured
+            // -5% at the Qwen3-8B chunked-prefill shape).
+            __builtin_amdgcn_s_setprio(1);
 #pragma unroll
             for (int kk = 0; kk < KK; kk++)
 #pragma unroll
@@ -343,6 +349,7 @@ __global__ __launch_bounds__(NW * 64, PrefillOcc<D>::kWavesPerSimd) void pa_pref
                 __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
             }
             __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+            __builtin_amdgcn_s_setprio(0);
         }
         float sv[NS];   // scores relative to mofs
 #pragma unroll
@@ -414,6 +421,7 @@ __global__ __launch_bounds__(NW * 64, PrefillOcc<D>::kWavesPerSimd) void pa_pref
         // 16st + 4hh + i/4 (then + 8) at dims 32m + 16((l/16)%2) + 4(i%4) and
         // receives dim 32m + l%32 of the 4 cells
         const int gi = lane & 15, vr = 4 * hh + (gi >> 2), vb0 = (16 * ((lane >> 4) & 1) + 4 * (gi & 3)) * 2;
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int st = 0; st < 2 * NH; st++)
 #pragma unroll
@@ -431,6 +439,7 @@ __global__ __launch_bounds__(NW * 64, PrefillOcc<D>::kWavesPerSimd) void pa_pref
             __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
         }
         __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
+        __builtin_amdgcn_s_setprio(0);
     };
 
     if (c_lo < c_hi) {

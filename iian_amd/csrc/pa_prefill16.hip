@@ -255,6 +255,9 @@ __global__ __launch_bounds__(NW * 64, (D == 128 && KVT == 1) ? 4 : (D <= 128 ? 2
 #pragma unroll
         for (int rt = 0; rt < NRT; rt++) {
             float sv[8];
+            // issue priority up for the MFMA clusters, so that the other wave
+            // on the SIMD runs its softmax in their shadow
+            __builtin_amdgcn_s_setprio(1);
 #pragma unroll
             for (int h = 0; h < 2; h++) {
                 f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -276,6 +279,7 @@ __global__ __launch_bounds__(NW * 64, (D == 128 && KVT == 1) ? 4 : (D <= 128 ? 2
 #pragma unroll
                 for (int i = 0; i < 4; i++) sv[4 * h + i] = acc[i];
             }
+            __builtin_amdgcn_s_setprio(0);
             if (p.softcap > 0.f) {
 #pragma unroll
                 for (int e = 0; e < 8; e++) sv[e] = p.softcap * tanhf(sv[e] * p.softcap_inv) * kLog2e;
@@ -324,12 +328,14 @@ __global__ __launch_bounds__(NW * 64, (D == 128 && KVT == 1) ? 4 : (D <= 128 ? 2
             pa[rt] = __builtin_bit_cast(f16x8, pk);
         }
         const char *vrow = Vl + (4 * g + (n >> 2)) * VSTRIDE + 8 * (n & 3);
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int m = 0; m < NPV; m++) {
             const f16x8 vb = lds_tr_b16x8_16(vrow + 32 * m, vrow + 16 * VSTRIDE + 32 * m);
 #pragma unroll
             for (int rt = 0; rt < NRT; rt++) o[rt][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[rt], vb, o[rt][m], 0, 0, 0);
         }
+        __builtin_amdgcn_s_setprio(0);
     };
 
     if (c_lo < c_hi) {

@@ -157,6 +157,11 @@ SMALL = {
     "prefix_shared": (32, 8, 128, [1200, 1100, 900, 300], [128, 64, 1, 1],
                       {"shared_blocks": 32, "shared_seqs": 3}),
     "block_size_32": (8, 2, 128, [500, 61], [1, 40], {"bs": 32}),
+    # f16 prefill tiles loaded with a scalar block base: 64-cell blocks with a
+    # window that starts tiles at odd multiples of 32 (a tile's cells span two
+    # blocks), and the smallest block size
+    "swa_prefill_d128_bs64": (8, 2, 128, [2000, 1200], [256, 100], {"n_swa": 480, "bs": 64}),
+    "prefill_d128_bs8": (8, 2, 128, [700, 300], [200, 64], {"bs": 8}),
     "random_positions": (8, 2, 64, [300, 200], [6, 40], {"pos_mode": "random"}),
     # Q8_0 pools (decode / spec-verify kernel)
     "q8_decode_gqa4_d128": (32, 8, 128, [513, 77, 2048, 33], [1, 1, 1, 1], {"k_type": Q8_0}),
