@@ -202,6 +202,10 @@ __device__ __forceinline__ void q8_piece(const AttnParams &p, Q8Lds<D> &lds, con
 
             // S^T = sum_blocks d_K[cell] * (K_int Q^T)
             f32x4 sacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+            // issue priority up for the MFMA clusters (QK^T here, PV below), so
+            // that the other wave on the SIMD stages or runs its softmax in
+            // their shadow (measured -1.5% at config 4)
+            __builtin_amdgcn_s_setprio(1);
 #pragma unroll
             for (int h = 0; h < 2; h++) {
                 const int cr = 8 * (n >> 2) + 4 * h + (n & 3);
@@ -216,6 +220,7 @@ __device__ __forceinline__ void q8_piece(const AttnParams &p, Q8Lds<D> &lds, con
                 }
             }
 
+            __builtin_amdgcn_s_setprio(0);
             const bool full = tile + kTile <= w.L && (!p.causal || tile + kTile - 1 <= w.pmin) &&
                               (p.n_swa <= 0 || w.pmax - tile < p.n_swa);
             float sv[8];
@@ -266,6 +271,7 @@ __device__ __forceinline__ void q8_piece(const AttnParams &p, Q8Lds<D> &lds, con
 
             // O += (P * d_V) V_int, one Q8_0 block (two 16-dim MFMAs) at a time
             const char *vrow = lds.v + (8 * g + (n >> 2)) * STRIDE + 8 * (n & 3);
+            __builtin_amdgcn_s_setprio(1);
 #pragma unroll
             for (int b = 0; b < NB; b++) {
                 const f32x4 d0 = *(const f32x4 *) &lds.vs[b][8 * g];
@@ -280,6 +286,7 @@ __device__ __forceinline__ void q8_piece(const AttnParams &p, Q8Lds<D> &lds, con
                     o[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pb, vb, o[m], 0, 0, 0);
                 }
             }
+            __builtin_amdgcn_s_setprio(0);
         }
     }
     if (pc.t0 == 0 && hk == 0 && threadIdx.x == 0) p.seg_info[pc.seg] = make_int2(pc.rec, pc.pieces);
