@@ -19,12 +19,13 @@
 //              f16 rows go to LDS, the block scales d to LDS as f32.
 //   QK^T       one v_mfma_f32_16x16x32_f16 per Q8_0 block (k-step = block),
 //              scaled by the K block's d per cell in fp32 afterwards
-//   PV         V^T operands via ds_read_b64_tr_b16; each PV MFMA covers 16
-//              dims of one block, so the V block scale is folded into P
-//              (per cell, f32 multiply before the f16 conversion of P)
+//   PV         V staged as f16(q*d), the correctly rounded dequantised
+//              value (both factors exact in f16); V^T operands via
+//              ds_read_b64_tr_b16
 //
-// So the dequantised value q*d (ggml-quants.c:553-567) enters the arithmetic
-// with q and d exact; rounding happens only where the f16 kernel rounds (q, P).
+// So K enters the scores as q*d (ggml-quants.c:553-567) with q and d exact and
+// the product in fp32, as in the reference's dequantised path; V enters as
+// f16(q*d), rounded once as P is.
 //
 // Memory order: a head slice is 34*D/32 bytes, so the slices of neighbouring
 // kv heads share cache lines.  The workgroups of one group are therefore
@@ -60,7 +61,6 @@ struct Q8Lds {
     __attribute__((aligned(16))) char k[Q8Shape<D>::TILE_BYTES];
     __attribute__((aligned(16))) char v[Q8Shape<D>::TILE_BYTES];
     __attribute__((aligned(16))) float ks[Q8Shape<D>::NB][kTile];
-    __attribute__((aligned(16))) float vs[Q8Shape<D>::NB][kTile];
 };
 
 // Raw Q8_0 bytes of one tile of one pool: lane l holds blocks [part*NBL,
@@ -83,8 +83,10 @@ __device__ __forceinline__ void q8_load_raw(const AttnParams &p, const char *poo
 
 // Converts a lane's raw window into f16 rows (tile_lds[cell][D]) and f32 block
 // scales (sc[block][cell]).  sh = byte offset of the lane's first block in the
-// window (0, or 2 for the second lane of a cell when D == 64).
-template <int D>
+// window (0, or 2 for the second lane of a cell when D == 64).  DEQ (V): the
+// rows hold f16(q*d), the correctly rounded dequantised value (both factors
+// are exact in f16), and no scales are written.
+template <int D, bool DEQ>
 __device__ __forceinline__ void q8_stage(const uint32_t (&raw)[Q8Shape<D>::W], int sh, char *tile_lds,
                                          float (*sc)[kTile]) {
     using Q = Q8Shape<D>;
@@ -112,12 +114,18 @@ __device__ __forceinline__ void q8_stage(const uint32_t (&raw)[Q8Shape<D>::W], i
             for (int k = 0; k < 8; k++)
                 q32[k] = sh ? raw[k + 1] : __builtin_amdgcn_alignbyte(raw[k + 1], raw[k], 2);
         }
-        sc[blk][cell] = (float) __builtin_bit_cast(_Float16, (uint16_t) dbits);
+        const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t) dbits);
+        if constexpr (!DEQ) sc[blk][cell] = (float) d;
+        const f16x2 d2 = {d, d};
         u32x4 h[4];
 #pragma unroll
         for (int k = 0; k < 8; k++) {
             uint32_t lo, hi;
             i8x4_to_f16(q32[k], lo, hi);
+            if constexpr (DEQ) {
+                lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, lo) * d2);
+                hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, hi) * d2);
+            }
             h[k >> 1][2 * (k & 1)] = lo;
             h[k >> 1][2 * (k & 1) + 1] = hi;
         }
@@ -179,8 +187,6 @@ __device__ __forceinline__ void q8_piece(const AttnParams &p, Q8Lds<D> &lds, con
         const bool stage_k = NW == 1 || wave == 0;
         const char *pool0 = stage_k ? p.k_pool : p.v_pool;
         const int64_t row0 = stage_k ? p.k_row : p.v_row;
-        char *dst0 = stage_k ? lds.k : lds.v;
-        float(*sc0)[kTile] = stage_k ? lds.ks : lds.vs;
         const int sh = (Q::SH_MAX == 0) ? 0 : ((hk * Q::HS + (lane & 1) * (34 * Q::NBL)) & 3);
         uint32_t raw[NRAW][Q::W];
         q8_load_raw<D>(p, pool0, row0, tw, w.L, hk, cb, raw[0]);
@@ -189,8 +195,9 @@ __device__ __forceinline__ void q8_piece(const AttnParams &p, Q8Lds<D> &lds, con
             const int next = tile + kTile;
             const bool has_next = next < ce;
             lds_barrier<NW>();   // every wave is done reading the previous tile
-            q8_stage<D>(raw[0], sh, dst0, sc0);
-            if constexpr (NRAW == 2) q8_stage<D>(raw[1], sh, lds.v, lds.vs);
+            if (stage_k) q8_stage<D, false>(raw[0], sh, lds.k, lds.ks);   // K: exact int8 values, f32 scales
+            else q8_stage<D, true>(raw[0], sh, lds.v, nullptr);          // V: f16(q*d)
+            if constexpr (NRAW == 2) q8_stage<D, true>(raw[1], sh, lds.v, nullptr);
             if (has_next && ((min(next + kTile - 1, w.L - 1) >> p.bs_log2) - tw.first) >= 64)
                 table_load(p, s, next >> p.bs_log2, w.L, tw);
             if (has_next) {
@@ -269,22 +276,16 @@ __device__ __forceinline__ void q8_piece(const AttnParams &p, Q8Lds<D> &lds, con
             }
             l_run += ps;
 
-            // O += (P * d_V) V_int, one Q8_0 block (two 16-dim MFMAs) at a time
+            // O += P V, V staged as f16(q*d)
             const char *vrow = lds.v + (8 * g + (n >> 2)) * STRIDE + 8 * (n & 3);
+            const u32x4 pk = {pack_f16x2(pv[0], pv[1]), pack_f16x2(pv[2], pv[3]), pack_f16x2(pv[4], pv[5]),
+                              pack_f16x2(pv[6], pv[7])};
+            const f16x8 pb = __builtin_bit_cast(f16x8, pk);
             __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-            for (int b = 0; b < NB; b++) {
-                const f32x4 d0 = *(const f32x4 *) &lds.vs[b][8 * g];
-                const f32x4 d1 = *(const f32x4 *) &lds.vs[b][8 * g + 4];
-                const u32x4 pk = {pack_f16x2(pv[0] * d0[0], pv[1] * d0[1]), pack_f16x2(pv[2] * d0[2], pv[3] * d0[3]),
-                                  pack_f16x2(pv[4] * d1[0], pv[5] * d1[1]), pack_f16x2(pv[6] * d1[2], pv[7] * d1[3])};
-                const f16x8 pb = __builtin_bit_cast(f16x8, pk);
-#pragma unroll
-                for (int mm = 0; mm < 2; mm++) {
-                    const int m = 2 * b + mm;
-                    const f16x8 vb = lds_tr_b16x8_q8(vrow + 32 * m, vrow + 4 * STRIDE + 32 * m);
-                    o[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pb, vb, o[m], 0, 0, 0);
-                }
+            for (int m = 0; m < NPV; m++) {
+                const f16x8 vb = lds_tr_b16x8_q8(vrow + 32 * m, vrow + 4 * STRIDE + 32 * m);
+                o[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pb, vb, o[m], 0, 0, 0);
             }
             __builtin_amdgcn_s_setprio(0);
         }
