@@ -243,8 +243,23 @@ __device__ __forceinline__ void lds_barrier() {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-__device__ __forceinline__ bool cell_masked(int c, int L, int prow, int causal, int n_swa) {
-    return c >= L || (causal && c > prow) || (n_swa > 0 && prow - c >= n_swa);
+// The cells base + off, off in [0, span), that a query row at position prow
+// sees, as one range of offsets [lo, lo + width).  Cell c is visible when
+// c < L, c <= prow under the causal mask, and prow - c < n_swa under a
+// sliding window (paged_attn.cpp:124); each condition is a bound on off.  Per cell the test is then one subtract and one unsigned
+// compare, with no branch (cell_visible).
+struct CellWindow {
+    int lo;
+    uint32_t width;
+};
+__device__ __forceinline__ CellWindow cell_window(int base, int span, int L, int prow, int causal, int n_swa) {
+    int hi = min(span, L - base);
+    if (causal) hi = min(hi, prow + 1 - base);
+    const int lo = n_swa > 0 ? max(0, prow - n_swa + 1 - base) : 0;
+    return {lo, (uint32_t) max(hi - lo, 0)};
+}
+__device__ __forceinline__ bool cell_visible(const CellWindow &cw, int off) {
+    return (uint32_t) (off - cw.lo) < cw.width;
 }
 
 __device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {

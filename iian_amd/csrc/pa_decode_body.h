@@ -167,9 +167,9 @@ __device__ __forceinline__ void decode_piece(const AttnParams &p, const SeqWindo
                     for (int e = 0; e < 8; e++) sv[e] = p.softcap * tanhf(sv[e] * p.softcap_inv) * kLog2e;
                 }
                 if (!full) {
+                    const CellWindow cw = cell_window(tile + 8 * g, 8, w.L, prow[rt], p.causal, p.n_swa);
 #pragma unroll
-                    for (int e = 0; e < 8; e++)
-                        if (cell_masked(tile + 8 * g + e, w.L, prow[rt], p.causal, p.n_swa)) sv[e] = -INFINITY;
+                    for (int e = 0; e < 8; e++) sv[e] = cell_visible(cw, e) ? sv[e] : -INFINITY;
                 }
                 float mt = sv[0];
 #pragma unroll

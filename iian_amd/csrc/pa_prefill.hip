@@ -361,11 +361,12 @@ __global__ __launch_bounds__(NW * 64, PrefillOcc<D>::kWavesPerSimd) void pa_pref
             for (int e = 0; e < NS; e++) sv[e] = p.softcap * tanhf(sv[e] * p.softcap_inv) * kLog2e;
         }
         if (!full) {
+            // score e is cell tile + 4hh + 32(e/16) + 8((e%16)/4) + e%4
+            const CellWindow cw = cell_window(tile + 4 * hh, PT, L, prow, p.causal, p.n_swa);
 #pragma unroll
             for (int e = 0; e < NS; e++) {
                 const int r = e & 15;
-                if (cell_masked(tile + 32 * (e >> 4) + 8 * (r >> 2) + 4 * hh + (r & 3), L, prow, p.causal, p.n_swa))
-                    sv[e] = -INFINITY;
+                sv[e] = cell_visible(cw, 32 * (e >> 4) + 8 * (r >> 2) + (r & 3)) ? sv[e] : -INFINITY;
             }
         }
         // Lazy rescale: the row's reference max m_run moves only when a score

@@ -285,9 +285,9 @@ __global__ __launch_bounds__(NW * 64, (D == 128 && KVT == 1) ? 4 : (D <= 128 ? 2
                 for (int e = 0; e < 8; e++) sv[e] = p.softcap * tanhf(sv[e] * p.softcap_inv) * kLog2e;
             }
             if (!full) {
+                const CellWindow cw = cell_window(tile + 8 * g, 8, L, prow[rt], p.causal, p.n_swa);
 #pragma unroll
-                for (int e = 0; e < 8; e++)
-                    if (cell_masked(tile + 8 * g + e, L, prow[rt], p.causal, p.n_swa)) sv[e] = -INFINITY;
+                for (int e = 0; e < 8; e++) sv[e] = cell_visible(cw, e) ? sv[e] : -INFINITY;
             }
             // Lazy rescale: the row's reference max m_run moves only when a
             // score exceeds it by more than kRescaleSlack; the test is on the

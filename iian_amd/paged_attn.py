@@ -209,9 +209,10 @@ def workspace_size(n_tokens: int, n_seqs: int, n_head: int, n_head_kv: int, head
 
 def new_workspace(n_tokens: int, n_seqs: int, n_head: int, n_head_kv: int, head_dim_v: int, max_blocks: int,
                   block_size: int, device="cuda") -> torch.Tensor:
-    """A workspace for build_paged_attn, reusable across calls on one stream."""
+    """A workspace for build_paged_attn, reusable across calls on one stream
+    (it needs no initialisation)."""
     n = workspace_size(n_tokens, n_seqs, n_head, n_head_kv, head_dim_v, max_blocks, block_size)
-    return torch.zeros(n, dtype=torch.uint8, device=device)
+    return torch.empty(n, dtype=torch.uint8, device=device)
 
 
 def build_paged_attn(q: torch.Tensor, k_cache: KVPool, v_cache: KVPool, n_head_kv: int,
@@ -241,7 +242,7 @@ def build_paged_attn(q: torch.Tensor, k_cache: KVPool, v_cache: KVPool, n_head_k
     max_blocks = int(batch.block_tables.shape[1])
     need = workspace_size(T, batch.n_seqs, H, n_head_kv, Dv, max_blocks, batch.block_size)
     if workspace is None:
-        workspace = torch.zeros(need, dtype=torch.uint8, device=q.device)
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
     elif workspace.numel() < need:
         raise ValueError(f"workspace holds {workspace.numel()} bytes, {need} needed")
     lib = _lib.load()

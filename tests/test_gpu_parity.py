@@ -144,6 +144,7 @@ SMALL = {
     "decode_gqa4_d128": (32, 8, 128, [513, 77, 2048, 33], [1, 1, 1, 1], {}),            # decode + stream-K merge
     "decode_gqa2_d256": (16, 8, 256, [1500, 40], [1, 1], {}),
     "decode_long_splits": (8, 2, 128, [9000, 5000], [1, 1], {}),                        # 18 splits
+    "decode_one_long_seq": (32, 8, 128, [32000], [1], {}),          # 125 pieces per (sequence, kv head)
     "spec_verify_5": (32, 8, 128, [700, 101, 4101], [5, 5, 5], {}),                     # decode, 2 row tiles
     "spec_verify_d64": (14, 2, 64, [300, 90], [3, 4], {}),
     "prefill_d128": (32, 8, 128, [600, 200], [512, 70], {}),                            # prefill kernel
@@ -171,6 +172,7 @@ SMALL = {
     "q8_decode_gqa2_d256": (16, 8, 256, [1500, 40], [1, 1], {"k_type": Q8_0}),
     "q8_swa_d256": (16, 8, 256, [3000, 900], [1, 2], {"k_type": Q8_0, "n_swa": 1024}),
     "q8_long_splits": (8, 2, 128, [9000, 5000], [1, 1], {"k_type": Q8_0}),
+    "q8_spec_one_long_seq": (32, 8, 128, [32000], [5], {"k_type": Q8_0}),   # 250 pieces x 2 row tiles
     "q8_block_size_32": (8, 2, 128, [500, 61], [1, 4], {"k_type": Q8_0, "bs": 32}),
     "q8_softcap": (8, 2, 128, [333, 77], [1, 3], {"k_type": Q8_0, "softcap": 30.0}),
     # Q8_0 pools through the prefill kernel
@@ -279,6 +281,68 @@ def test_workspace_reuse_across_calls(pa, oracle):
         torch.cuda.synchronize()
         e = row_rel_err(got.cpu().numpy(), oracle_attention(oracle, c))
         assert e.max() <= TOL, (it, e.max())
+
+
+@pytest.mark.parametrize("k_type,nq", [(F16, 1), (Q8_0, 5)])
+def test_split_merge_with_garbage_workspace(pa, oracle, k_type, nq):
+    """The workspace needs no initialisation: every record and segment entry
+    the merge reads is written earlier in the same call.  Filled with 0xff,
+    with random bytes, or zeroed, the workspace gives the same bits and the
+    oracle's result."""
+    banner(f"split merge over garbage workspaces k_type={k_type} nq={nq}")
+    rng = np.random.default_rng(48 + nq)
+    c = make_case(rng, 32, 8, 128, [6000, 700, 3000, 2500], [nq] * 4, k_type=k_type, quantize=oracle.quantize_q8_0)
+    k, v, batch = to_device(pa, c)
+    prm = pa.PagedAttnParams(scale=c.scale)
+    q = torch.as_tensor(c.q).cuda()
+    ws = pa.new_workspace(c.T, 4, c.H, c.Hkv, c.D, c.bt.shape[1], c.bs)
+    outs = []
+    for fill in ("ff", "random", "zero"):
+        if fill == "ff":
+            ws.fill_(255)
+        elif fill == "random":
+            ws.copy_(torch.randint(0, 256, ws.shape, dtype=torch.uint8, generator=torch.Generator().manual_seed(7)))
+        else:
+            ws.zero_()
+        outs.append(pa.build_paged_attn(q, k, v, c.Hkv, prm, batch, workspace=ws).cpu().numpy())
+    assert row_rel_err(outs[0], oracle_attention(oracle, c)).max() <= TOL
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+
+
+@pytest.mark.parametrize("k_type,nq", [(F16, 1), (Q8_0, 5)])
+def test_graph_replays_match_eager(pa, oracle, k_type, nq):
+    """A call captured in a graph (decode kernel and merge) and replayed four
+    times, with eager calls of another batch on the same workspace in
+    between, gives the eager call's bits on every replay."""
+    banner(f"graph replays k_type={k_type} nq={nq}")
+    rng = np.random.default_rng(49 + nq)
+    c = make_case(rng, 32, 8, 128, [5000, 700, 3000, 64], [nq] * 4, k_type=k_type, quantize=oracle.quantize_q8_0)
+    k, v, batch = to_device(pa, c)
+    prm = pa.PagedAttnParams(scale=c.scale)
+    q = torch.as_tensor(c.q).cuda()
+    ws = pa.new_workspace(c.T, 4, c.H, c.Hkv, c.D, c.bt.shape[1], c.bs)
+    eager = pa.build_paged_attn(q, k, v, c.Hkv, prm, batch).cpu().numpy()
+    assert row_rel_err(eager, oracle_attention(oracle, c)).max() <= TOL
+    q2 = torch.as_tensor(rng.standard_normal(c.q.shape).astype(np.float32)).cuda()
+    other = pa.build_paged_attn(q2, k, v, c.Hkv, prm, batch).cpu().numpy()
+    out = torch.empty_like(q)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        pa.build_paged_attn(q, k, v, c.Hkv, prm, batch, out=out, workspace=ws)   # warm-up outside the capture
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        pa.build_paged_attn(q, k, v, c.Hkv, prm, batch, out=out, workspace=ws)
+    for it in range(4):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy(), eager), it
+        o2 = pa.build_paged_attn(q2, k, v, c.Hkv, prm, batch, workspace=ws)
+        torch.cuda.synchronize()
+        assert np.array_equal(o2.cpu().numpy(), other), it
 
 
 def test_attention_bad_block_id_is_clamped_and_flagged(pa):
