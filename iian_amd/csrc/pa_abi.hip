@@ -198,6 +198,11 @@ int iian_pa_attention(void *stream, const float *q, const void *k_pool, const vo
     int64_t kr, vr;
     if (row_bytes(type_k, (int64_t) n_head_kv * head_dim, kr) || row_bytes(type_v, (int64_t) n_head_kv * head_dim_v, vr))
         return IIAN_PA_ERR_ARG;
+    // The kernels index pool rows with 32-bit cell numbers and row lengths
+    // (pool_off): 2^32 cells of the smallest supported row (68 bytes, one
+    // Q8_0 head of size 64) are 272 GiB, more than an MI355X's 288 GB hold.
+    if (((int64_t) num_blocks << bs_log2) > ((int64_t) 1 << 32) || kr != vr || kr > (int64_t) UINT32_MAX)
+        return IIAN_PA_ERR_UNSUPPORTED;
     p.k_row = kr;
     p.v_row = vr;
     p.max_blocks = max_blocks;

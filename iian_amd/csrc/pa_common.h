@@ -35,8 +35,8 @@ struct AttnParams {
     float *part_ml;             // (reference max in log2 units, sum) per record row
     int2 *seg_info;             // per segment: (first record, pieces), written by the segment's first piece
     int32_t *err;               // nullable error word
-    int64_t k_row;              // bytes per K pool row
-    int64_t v_row;
+    int64_t k_row;              // bytes per K pool row (< 2^32)
+    int64_t v_row;              // equal to k_row: K and V share type and head size
     int64_t rec_stride;         // floats per record of part_o
     int32_t max_blocks;
     int32_t num_blocks;
@@ -226,9 +226,16 @@ __device__ __forceinline__ void table_load(const AttnParams &p, int s, int first
 }
 
 // Pool row of cell c (c <= L-1) whose 8-cell group starts at grp (grp <= c, same block).
-__device__ __forceinline__ int64_t table_row(const AttnParams &p, const TableWindow &tw, int grp_clamped, int c) {
+__device__ __forceinline__ uint32_t table_row(const AttnParams &p, const TableWindow &tw, int grp_clamped, int c) {
     const int blk = __shfl(tw.id, (grp_clamped >> p.bs_log2) - tw.first);
-    return ((int64_t) blk << p.bs_log2) | (c & ((1 << p.bs_log2) - 1));
+    return ((uint32_t) blk << p.bs_log2) | (uint32_t) (c & ((1 << p.bs_log2) - 1));
+}
+
+// Byte offset of pool row `row`.  The host admits only pools whose cell
+// indices and row lengths fit in 32 bits (iian_pa_attention), so this is one
+// 32x32 -> 64-bit multiply (v_mad_u64_u32) instead of a 64x64 product.
+__device__ __forceinline__ uint64_t pool_off(uint32_t row, int64_t row_bytes) {
+    return (uint64_t) row * (uint32_t) row_bytes;
 }
 
 // Orders this wave's LDS accesses before every wave's accesses after it

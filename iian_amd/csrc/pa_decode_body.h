@@ -43,8 +43,8 @@ __device__ __forceinline__ void load_k(const AttnParams &p, const TableWindow &t
 #pragma unroll
     for (int h = 0; h < 2; h++) {
         const int c = min(tile + 8 * (n >> 2) + 4 * h + (n & 3), last);
-        const int64_t row = table_row(p, tw, grp, c);
-        const char *base = p.k_pool + row * p.k_row + (int64_t) hk * D * 2 + g * 16;
+        const uint32_t row = table_row(p, tw, grp, c);
+        const char *base = p.k_pool + pool_off(row, p.k_row) + (hk * D * 2 + g * 16);
 #pragma unroll
         for (int ks = 0; ks < D / 32; ks++) r.k[h][ks] = stream_load<D>((const u32x4 *) (base + ks * 64));
     }
@@ -61,8 +61,8 @@ __device__ __forceinline__ void load_v(const AttnParams &p, const TableWindow &t
 #pragma unroll
     for (int e = 0; e < 8; e++) {
         const int c = min(tile + 8 * g + e, last);
-        const int64_t row = table_row(p, tw, grp, c);
-        const uint32_t *src = (const uint32_t *) (p.v_pool + row * p.v_row + (int64_t) hk * D * 2 + n * (D / 8));
+        const uint32_t row = table_row(p, tw, grp, c);
+        const uint32_t *src = (const uint32_t *) (p.v_pool + pool_off(row, p.v_row) + (hk * D * 2 + n * (D / 8)));
         if constexpr (VW == 2) {
             const u32x2 x = stream_load<D>((const u32x2 *) src);
             r.v[e][0] = x[0];

@@ -74,9 +74,9 @@ __device__ __forceinline__ void q8_load_raw(const AttnParams &p, const char *poo
     using Q = Q8Shape<D>;
     const int lane = threadIdx.x & 63;
     const int c = min(tile + (lane >> 1), L - 1);
-    const int64_t row = table_row(p, tw, c, c);
+    const uint32_t row = table_row(p, tw, c, c);
     const int off = hk * Q::HS + (lane & 1) * (34 * Q::NBL);
-    const uint32_t *src = (const uint32_t *) (pool + row * row_bytes + (off & ~3));
+    const uint32_t *src = (const uint32_t *) (pool + pool_off(row, row_bytes) + (off & ~3));
 #pragma unroll
     for (int i = 0; i < Q::W; i++) raw[i] = src[i];
 }

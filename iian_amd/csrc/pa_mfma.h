@@ -47,6 +47,29 @@ __device__ __forceinline__ int tile_off(int r, int b, int stride) {
 
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
+// Two transpose reads at LDS byte addresses a0, a1.  Callers that read
+// several tiles from one lane base pass the base through opaque() first, so
+// that the constant tile offsets become ds_read immediates instead of a VALU
+// add per read (the compiler otherwise merges them into a scalar and adds
+// that to the lane base before every read).
+__device__ __forceinline__ f16x8 lds_tr_b16x8_at(uint32_t a0, uint32_t a1) {
+    const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *) (uintptr_t) a0);
+    const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *) (uintptr_t) a1);
+    typedef short s16x8 __attribute__((ext_vector_type(8)));
+    const s16x8 c = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+    return __builtin_bit_cast(f16x8, c);
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void *p) { return (uint32_t) (uintptr_t) p; }
+
+typedef __attribute__((address_space(3))) f16x8 lds_f16x8;
+__device__ __forceinline__ f16x8 lds_read_f16x8(uint32_t a) { return *(const lds_f16x8 *) (uintptr_t) a; }
+
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
 __device__ __forceinline__ f16x8 lds_tr_b16x8(const char *p0, const char *p1) {
     const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *) (uintptr_t) p0);
     const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *) (uintptr_t) p1);

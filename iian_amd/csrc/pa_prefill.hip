@@ -193,11 +193,11 @@ __global__ __launch_bounds__(NW * 64, PrefillOcc<D>::kWavesPerSimd) void pa_pref
                 const int qi_t = item / (PT * NB), qi_cell = (item % (PT * NB)) / NB, qi_b = item % NB;
                 const int c = min(tile + qi_cell, L - 1);
                 const int32_t blk = __shfl(tw.id, (c >> p.bs_log2) - tw.first);
-                const int64_t row = ((int64_t) blk << p.bs_log2) | (c & bs_mask);
+                const uint32_t row = ((uint32_t) blk << p.bs_log2) | (uint32_t) (c & bs_mask);
                 if (item < ITEMS) {
                     const int start = hk * NB * 34 + 34 * qi_b;
-                    const uint32_t *src = (const uint32_t *) ((qi_t ? p.v_pool + row * p.v_row
-                                                                     : p.k_pool + row * p.k_row) + (start & ~3));
+                    const uint32_t *src = (const uint32_t *) ((qi_t ? p.v_pool : p.k_pool) + pool_off(row, p.k_row) +
+                                                              (start & ~3));
 #pragma unroll
                     for (int i = 0; i < 9; i++) qraw[it][i] = src[i];
                 }
@@ -209,9 +209,10 @@ __global__ __launch_bounds__(NW * 64, PrefillOcc<D>::kWavesPerSimd) void pa_pref
                 const int cell = q / (D / 8), col = q % (D / 8);
                 const int c = min(tile + cell, L - 1);
                 const int32_t blk = __shfl(tw.id, (c >> p.bs_log2) - tw.first);
-                const int64_t row = ((int64_t) blk << p.bs_log2) | (c & bs_mask);
-                kst[j] = *(const u32x4 *) (p.k_pool + row * p.k_row + head_off + col * 16);
-                vst[j] = *(const u32x4 *) (p.v_pool + row * p.v_row + head_off + col * 16);
+                const uint32_t row = ((uint32_t) blk << p.bs_log2) | (uint32_t) (c & bs_mask);
+                const uint64_t off = pool_off(row, p.k_row) + (uint32_t) (head_off + col * 16);
+                kst[j] = *(const u32x4 *) (p.k_pool + off);
+                vst[j] = *(const u32x4 *) (p.v_pool + off);
             }
         }
     };
@@ -228,12 +229,12 @@ __global__ __launch_bounds__(NW * 64, PrefillOcc<D>::kWavesPerSimd) void pa_pref
             const int r = b / (2 * D), slot = (b % (2 * D)) >> 4;
             const int c = min(tile + r, L - 1);
             const int32_t blk = __shfl(tw.id, (c >> p.bs_log2) - tw.first);
-            const int64_t row = ((int64_t) blk << p.bs_log2) | (c & bs_mask);
-            const int64_t col = head_off + 16 * (slot ^ swz(r & 15));
+            const uint32_t row = ((uint32_t) blk << p.bs_log2) | (uint32_t) (c & bs_mask);
+            const uint64_t off = pool_off(row, p.k_row) + (uint32_t) (head_off + 16 * (slot ^ swz(r & 15)));
             const uint32_t lk = __builtin_amdgcn_readfirstlane((uint32_t) (uintptr_t) (Kd + q * 1024));
             const uint32_t lv = __builtin_amdgcn_readfirstlane((uint32_t) (uintptr_t) (Vd + q * 1024));
-            lds_load16(p.k_pool + row * p.k_row + col, lk);
-            lds_load16(p.v_pool + row * p.v_row + col, lv);
+            lds_load16(p.k_pool + off, lk);
+            lds_load16(p.v_pool + off, lv);
         }
     };
     auto store_lds = [&](int buf) {
@@ -331,12 +332,15 @@ __global__ __launch_bounds__(NW * 64, PrefillOcc<D>::kWavesPerSimd) void pa_pref
             // first and the other's softmax VALU fills the MFMA shadow, instead
             // of both waves reaching their softmax at the same time (measured
             // -5% at the Qwen3-8B chunked-prefill shape).
+            uint32_t ka[KK];   // this tile's read bases of k-step kk (row n of half 0)
+#pragma unroll
+            for (int kk = 0; kk < KK; kk++) ka[kk] = opaque(lds_addr(Kl + tile_off<D, DMA>(n, 32 * kk + 16 * hh, KSTRIDE)));
             __builtin_amdgcn_s_setprio(1);
 #pragma unroll
             for (int kk = 0; kk < KK; kk++)
 #pragma unroll
                 for (int c = 0; c < NH; c++) {
-                    const f16x8 a = *(const f16x8 *) (Kl + 32 * c * KSTRIDE + tile_off<D, DMA>(n, 32 * kk + 16 * hh, KSTRIDE));
+                    const f16x8 a = lds_read_f16x8(ka[kk] + 32 * c * KSTRIDE);
                     sa[c] = mfma32(a, qv[kk], sa[c]);
                     sa[c] = mfma32(a, ql[kk], sa[c]);
                 }
@@ -422,14 +426,17 @@ __global__ __launch_bounds__(NW * 64, PrefillOcc<D>::kWavesPerSimd) void pa_pref
         // 16st + 4hh + i/4 (then + 8) at dims 32m + 16((l/16)%2) + 4(i%4) and
         // receives dim 32m + l%32 of the 4 cells
         const int gi = lane & 15, vr = 4 * hh + (gi >> 2), vb0 = (16 * ((lane >> 4) & 1) + 4 * (gi & 3)) * 2;
+        uint32_t va[NO][2];   // this tile's read bases of output tile m, rows vr and vr + 8
+#pragma unroll
+        for (int m = 0; m < NO; m++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) va[m][h] = opaque(lds_addr(Vl + tile_off<D, DMA>(vr + 8 * h, 64 * m + vb0, VSTRIDE)));
         __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int st = 0; st < 2 * NH; st++)
 #pragma unroll
             for (int m = 0; m < NO; m++) {
-                const char *v0 = Vl + 16 * st * VSTRIDE;
-                const f16x8 vb = lds_tr_b16x8(v0 + tile_off<D, DMA>(vr, 64 * m + vb0, VSTRIDE),
-                                              v0 + tile_off<D, DMA>(vr + 8, 64 * m + vb0, VSTRIDE));
+                const f16x8 vb = lds_tr_b16x8_at(va[m][0] + 16 * st * VSTRIDE, va[m][1] + 16 * st * VSTRIDE);
                 o[m] = mfma32(pa[st], vb, o[m]);
             }
         // V transpose reads run three MFMAs ahead of their use

@@ -177,10 +177,10 @@ __global__ __launch_bounds__(NW * 64, (D == 128 && KVT == 1) ? 4 : (D <= 128 ? 2
         if constexpr (Q8) {
             const int c = min(tile + qi_cell, L - 1);
             const int32_t blk = __shfl(tw.id, (c >> p.bs_log2) - tw.first);
-            const int64_t row = ((int64_t) blk << p.bs_log2) | (c & bs_mask);
+            const uint32_t row = ((uint32_t) blk << p.bs_log2) | (uint32_t) (c & bs_mask);
             if (qi_live) {
                 const int start = hk * NB * 34 + 34 * qi_b;
-                const uint32_t *src = (const uint32_t *) ((qi_t ? p.v_pool + row * p.v_row : p.k_pool + row * p.k_row) +
+                const uint32_t *src = (const uint32_t *) ((qi_t ? p.v_pool : p.k_pool) + pool_off(row, p.k_row) +
                                                           (start & ~3));
 #pragma unroll
                 for (int i = 0; i < 9; i++) qraw[i] = src[i];
@@ -192,9 +192,10 @@ __global__ __launch_bounds__(NW * 64, (D == 128 && KVT == 1) ? 4 : (D <= 128 ? 2
                 const int cell = q / (D / 8), col = q % (D / 8);
                 const int c = min(tile + cell, L - 1);
                 const int32_t blk = __shfl(tw.id, (c >> p.bs_log2) - tw.first);
-                const int64_t row = ((int64_t) blk << p.bs_log2) | (c & bs_mask);
-                kst[j] = *(const u32x4 *) (p.k_pool + row * p.k_row + head_off + col * 16);
-                vst[j] = *(const u32x4 *) (p.v_pool + row * p.v_row + head_off + col * 16);
+                const uint32_t row = ((uint32_t) blk << p.bs_log2) | (uint32_t) (c & bs_mask);
+                const uint64_t off = pool_off(row, p.k_row) + (uint32_t) (head_off + col * 16);
+                kst[j] = *(const u32x4 *) (p.k_pool + off);
+                vst[j] = *(const u32x4 *) (p.v_pool + off);
             }
         }
     };

@@ -89,7 +89,7 @@ def call_attention(lib, **over):
     ({"H": 6, "Hkv": 4}, -2), ({"Hkv": 0}, -2), ({"T": -1}, -2), ({"maxq": 5}, -2), ({"num_blocks": 0}, -2),
     ({"n_swa": -1}, -2), ({"softcap": -1.0}, -2), ({"scale": float("nan")}, -2), ({"q": 0x1004}, -2),
     ({"tk": 8, "tv": 8, "D": 96, "Dv": 96}, -3), ({"tk": 0, "tv": 0}, -3), ({"tk": 1, "tv": 0}, -3), ({"D": 96, "Dv": 96}, -3),
-    ({"bs": 12}, -3), ({"bs": 4}, -3),
+    ({"bs": 12}, -3), ({"bs": 4}, -3), ({"num_blocks": (1 << 28) + 1}, -3),   # more than 2^32 cells
     ({"ws": None}, -4), ({"ws_bytes": 16}, -4),
 ])
 def test_attention_rejects_invalid_arguments(lib, over, code):
