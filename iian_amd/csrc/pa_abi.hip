@@ -7,7 +7,10 @@
 #include "pa_launch.h"
 
 #include <algorithm>
+#include <atomic>
+#include <chrono>
 #include <cmath>
+#include <random>
 
 namespace {
 
@@ -33,7 +36,7 @@ constexpr int kDecodeWaves = kQ8DecodeWaves > kF16DecodeWaves ? kQ8DecodeWaves :
 int q8_waves_per_wg(int decode_rows) { return decode_rows > 16 ? 2 : 1; }   // NW of pa_decode_q8_kernel
 
 // Workspace: [partial records (numerators)][(m, l) per record row][segment
-// info], each section 256-byte aligned.  Sized for the record count of
+// info][merge counter per (sequence, kv head)], each section 256-byte aligned.  Sized for the record count of
 // either kernel at kDecodeRowsMax rows: the f16 kernel has at most
 // kF16DecodeWaves + S*Hkv one-head records, the Q8_0 kernel at most
 // kQ8DecodeWaves/Hkv + S records of Hkv heads.  A record is padded by 64 floats
@@ -42,7 +45,7 @@ int q8_waves_per_wg(int decode_rows) { return decode_rows > 16 ? 2 : 1; }   // N
 constexpr int kRecordPad = 64;
 
 struct WorkspaceLayout {
-    size_t o, ml, seg, total;
+    size_t o, ml, seg, ctr, total;
 };
 
 inline size_t align256(size_t v) { return (v + 255) & ~(size_t) 255; }
@@ -53,8 +56,22 @@ WorkspaceLayout workspace_layout(int32_t n_seqs, int32_t n_head_kv, int32_t head
     l.o = 0;
     l.ml = l.o + align256((rec_heads * kDecodeRowsMax * head_dim_v + rec_heads * kRecordPad) * sizeof(float));
     l.seg = l.ml + align256(rec_heads * kDecodeRowsMax * 2 * sizeof(float));
-    l.total = l.seg + align256((size_t) n_seqs * n_head_kv * sizeof(int2));
+    l.ctr = l.seg + align256((size_t) n_seqs * n_head_kv * sizeof(int2));
+    l.total = l.ctr + align256((size_t) n_seqs * n_head_kv * sizeof(uint64_t));
     return l;
+}
+
+// Tags of the mixed launch's merge counters: one per call, 48 bits, counting
+// up from a random start, so that workspace bytes the library never wrote
+// pass for a counter of the current call only with probability 2^-48 per
+// counter (the kernel treats any other tag as a count of zero).
+uint64_t next_epoch() {
+    static std::atomic<uint64_t> next{[] {
+        std::random_device rd;
+        const uint64_t t = (uint64_t) std::chrono::steady_clock::now().time_since_epoch().count();
+        return ((uint64_t) rd() << 32 ^ (uint64_t) rd()) ^ t * 0x9e3779b97f4a7c15ull;
+    }()};
+    return next.fetch_add(1, std::memory_order_relaxed) & ((1ull << 48) - 1);
 }
 
 // Side stream and fork/join events of one host thread for one device, created
@@ -238,13 +255,16 @@ int iian_pa_attention(void *stream, const float *q, const void *k_pool, const vo
     p.part_o = (float *) (ws + wl.o);
     p.part_ml = (float *) (ws + wl.ml);
     p.seg_info = (int2 *) (ws + wl.seg);
+    p.seg_ctr = (uint64_t *) (ws + wl.ctr);
+    p.epoch = next_epoch();
     hipStream_t st = (hipStream_t) stream;
     if (max_rows <= p.decode_rows)
         return launch_decode(p, head_dim, type_k, st) == hipSuccess ? IIAN_PA_OK : IIAN_PA_ERR_HIP;
 
     // Mixed batch over an f16 pool (head size 64 or 128): one launch holds the
     // prefill workgroups and, after them, the decode rows' stream-K workers,
-    // which fill the CUs the MFMA-bound prefill leaves; the merge follows.
+    // which fill the CUs the MFMA-bound prefill leaves, and merge their split
+    // segments themselves.
     if (type_k == IIAN_PA_TYPE_F16 && head_dim <= 128)
         return launch_mixed_f16(p, head_dim, max_rows, st) == hipSuccess ? IIAN_PA_OK : IIAN_PA_ERR_HIP;
 

@@ -34,10 +34,12 @@ struct AttnParams {
     float *part_o;              // stream-K partial records: numerators, rec_stride floats per record
     float *part_ml;             // (reference max in log2 units, sum) per record row
     int2 *seg_info;             // per segment: (first record, pieces), written by the segment's first piece
+    uint64_t *seg_ctr;          // per (sequence, kv head): (call epoch << 16) | pieces counted in (mixed launch)
     int32_t *err;               // nullable error word
     int64_t k_row;              // bytes per K pool row (< 2^32)
     int64_t v_row;              // equal to k_row: K and V share type and head size
     int64_t rec_stride;         // floats per record of part_o
+    uint64_t epoch;             // this call's tag for seg_ctr (48 bits)
     int32_t max_blocks;
     int32_t num_blocks;
     int32_t T, S, H, Hkv, gqa;
@@ -89,7 +91,8 @@ __device__ __forceinline__ int32_t phys_block(const AttnParams &p, int s, int b)
 // sequences they fall in, so every worker carries the same work however ragged
 // the contexts are.  The stretch of one worker inside one segment is a piece;
 // a segment with one piece writes its output directly, the others write
-// partial records merged by pa_merge_kernel.  Piece (worker w, segment seg) has
+// partial records merged by pa_merge_kernel (or, in the mixed prefill launch,
+// by the segment's last piece to finish: arrive_last).  Piece (worker w, segment seg) has
 // record w + seg: along the line either w or seg grows by one from piece to
 // piece, so records are unique and a segment's pieces hold consecutive ones.
 constexpr int kMinPieceTiles = 2;
@@ -148,10 +151,10 @@ __device__ __forceinline__ int wave_incl_scan(int v) {
 }
 
 // One piece of a worker's range: sequence s (window w), kv head hk, window
-// tiles [t0, t1), partial record rec, and the segment's piece count (1 = the
-// piece is the whole segment and writes the output itself).
+// tiles [t0, t1), partial record rec, the segment's first record rec0 and its
+// piece count (1 = the piece is the whole segment and writes the output itself).
 struct Piece {
-    int s, hk, t0, t1, rec, pieces, seg;
+    int s, hk, t0, t1, rec, rec0, pieces, seg;
 };
 
 // Calls body(w, piece) for each piece of worker `worker` (wave-uniform).
@@ -196,6 +199,7 @@ __device__ __forceinline__ void for_each_piece(const AttnParams &p, int worker, 
         const int seg_start = excl + (GROUPED ? 0 : pc.hk * w.nt);
         pc.seg = GROUPED ? s : s * p.Hkv + pc.hk;
         pc.rec = worker + pc.seg;
+        pc.rec0 = seg_start / per + pc.seg;   // record of the segment's first piece
         pc.pieces = (seg_start + w.nt - 1) / per - seg_start / per + 1;
         body(w, pc);
         start = seg_start + pc.t1;
@@ -209,6 +213,124 @@ __device__ __forceinline__ float *rec_o(const AttnParams &p, int rec, int hr, in
 }
 __device__ __forceinline__ float *rec_ml(const AttnParams &p, int rec, int hr, int r) {
     return p.part_ml + (((int64_t) rec * p.rec_heads + hr) * p.decode_rows + r) * 2;
+}
+
+// ---- Merge of a split segment inside the launch (mixed prefill launch) ----
+//
+// The L2s of MI355X's XCDs are not coherent with each other within a launch,
+// so the partial records are handed over in agent-scope operations: stores
+// and loads with the sc1 bit (written through to, and read from, the
+// device-coherent level).  A piece writes its record rows that way, waits for
+// them (s_waitcnt vmcnt(0)), then counts itself in on the segment's counter
+// (arrive_last); the piece that completes the count reads every record of the
+// segment with agent-scope loads and writes the output.  No release fence is
+// needed (on gfx950 an agent-scope release writes back the whole L2):
+// everything handed over travels in agent-scope operations, and the wait
+// orders them before the count.  The chain of memory round trips this puts
+// after a worker's last piece costs more than a merge launch when the decode
+// kernel runs alone, so only the mixed launch merges this way: there the
+// decode workers finish long before the prefill workgroups.
+__device__ __forceinline__ void store_pair_agent(float *ptr, float a, float b) {   // ptr 8-byte aligned
+    const uint64_t v = (uint64_t) __float_as_uint(a) | ((uint64_t) __float_as_uint(b) << 32);
+    __hip_atomic_store((uint64_t *) ptr, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float2 load_pair_agent(const float *ptr) {
+    const uint64_t v = __hip_atomic_load((uint64_t *) ptr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return make_float2(__uint_as_float((uint32_t) v), __uint_as_float((uint32_t) (v >> 32)));
+}
+
+// Counts the calling wave in on counter ctr after its record stores have
+// completed; true (wave-uniform) for the wave that brings the count to
+// `expected`.  A counter holding another epoch (another call, or workspace
+// bytes never written by this library) counts as zero, so the workspace needs
+// no initialisation.  The completing wave resets the counter to (epoch, 0),
+// which keeps replays of a captured launch, which reuse one epoch, correct.
+// The compare-and-swap loop ends: each failed attempt means another wave's
+// attempt succeeded, and at most `expected` waves use the counter per call.
+__device__ __forceinline__ bool arrive_last(uint64_t *ctr, uint64_t epoch, int expected) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's record stores are complete
+    uint32_t cnt = 0;
+    if ((threadIdx.x & 63) == 0) {
+        uint64_t old = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (;;) {
+            const uint64_t nw = (old >> 16) == epoch ? old + 1 : (epoch << 16) | 1u;
+            if (__hip_atomic_compare_exchange_strong(ctr, &old, nw, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT)) {
+                cnt = (uint32_t) (nw & 0xffffu);
+                break;
+            }
+        }
+        if (cnt == (uint32_t) expected) __hip_atomic_store(ctr, epoch << 16, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    cnt = __builtin_amdgcn_readfirstlane(__shfl(cnt, 0));
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // record loads only after the count
+    return cnt == (uint32_t) expected;
+}
+
+// Log-sum-exp merge of rows [row0, row0 + 16) of kv-head slot hr over the
+// segment's records rec0 .. rec0+np-1, written to the output rows of kv head
+// hk: out = sum_j 2^(m_j - m) O_j / sum_j 2^(m_j - m) l_j, m = max_j m_j
+// (rows every record left at m = -inf are all-masked and come out as zeros).
+// Lane (g, n) merges rows row0 + 4g + i, dims (D/16)n .. (D/16)n + D/16 - 1;
+// the loads of two records are issued together.
+template <int D>
+__device__ __forceinline__ void merge_tile16(const AttnParams &p, int rec0, int np, int hr, int row0, int M,
+                                             int q0, int hk) {
+    constexpr int DPL = D / 16;
+    constexpr int B = 2;
+    const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
+    float mx[4], ls[4], acc[4][DPL];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        mx[i] = -INFINITY;
+        ls[i] = 0.f;
+#pragma unroll
+        for (int d = 0; d < DPL; d++) acc[i][d] = 0.f;
+    }
+    for (int j0 = 0; j0 < np; j0 += B) {
+        float2 ml[B][4], ov[B][4][DPL / 2];
+#pragma unroll
+        for (int u = 0; u < B; u++) {
+            const int j = rec0 + min(j0 + u, np - 1);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int r = min(row0 + 4 * g + i, M - 1);   // rows >= M are never written
+                ml[u][i] = load_pair_agent(rec_ml(p, j, hr, r));
+                const float *op = rec_o(p, j, hr, r, D) + DPL * n;
+#pragma unroll
+                for (int c = 0; c < DPL / 2; c++) ov[u][i][c] = load_pair_agent(op + 2 * c);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < B; u++) {
+            if (j0 + u >= np) break;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float mn = fmaxf(mx[i], ml[u][i].x);
+                if (mn == -INFINITY) continue;
+                const float a = __builtin_amdgcn_exp2f(mx[i] - mn), b = __builtin_amdgcn_exp2f(ml[u][i].x - mn);
+                mx[i] = mn;
+                ls[i] = ls[i] * a + ml[u][i].y * b;
+#pragma unroll
+                for (int c = 0; c < DPL / 2; c++) {
+                    acc[i][2 * c] = acc[i][2 * c] * a + ov[u][i][c].x * b;
+                    acc[i][2 * c + 1] = acc[i][2 * c + 1] * a + ov[u][i][c].y * b;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int r = row0 + 4 * g + i;
+        if (r >= M) continue;
+        const int t = q0 + r / p.gqa, h = hk * p.gqa + r % p.gqa;
+        const float inv = ls[i] > 0.f ? 1.f / ls[i] : 0.f;
+        float *op = p.out + ((int64_t) t * p.H + h) * D + DPL * n;
+#pragma unroll
+        for (int d = 0; d < DPL; d += 4)
+            *(float4 *) (op + d) = make_float4(acc[i][d] * inv, acc[i][d + 1] * inv, acc[i][d + 2] * inv,
+                                               acc[i][d + 3] * inv);
+    }
 }
 
 // Block-table entries of 64 consecutive logical blocks of one sequence, one

@@ -81,7 +81,9 @@ __device__ __forceinline__ void load_v(const AttnParams &p, const TableWindow &t
 }
 
 // One piece: window tiles [pc.t0, pc.t1) of sequence pc.s at kv head pc.hk.
-template <int D, int NRT>
+// FUSED: a split segment is merged by its last piece to finish (arrive_last),
+// not by pa_merge_kernel.
+template <int D, int NRT, bool FUSED = false>
 __device__ __forceinline__ void decode_piece(const AttnParams &p, const SeqWindow &w, const Piece &pc) {
     constexpr int KS = D / 32;
     constexpr int DPL = D / 16;
@@ -222,7 +224,7 @@ __device__ __forceinline__ void decode_piece(const AttnParams &p, const SeqWindo
         }
     }
 
-    if (pc.t0 == 0 && lane == 0) p.seg_info[pc.seg] = make_int2(pc.rec, pc.pieces);
+    if (!FUSED && pc.t0 == 0 && lane == 0) p.seg_info[pc.seg] = make_int2(pc.rec, pc.pieces);
 #pragma unroll
     for (int rt = 0; rt < NRT; rt++) {
         float l = l_run[rt];
@@ -249,14 +251,29 @@ __device__ __forceinline__ void decode_piece(const AttnParams &p, const SeqWindo
                 const int r = rt * 16 + 4 * g + i;
                 if (r < M) {
                     float *op = rec_o(p, pc.rec, 0, r, D) + DPL * n;
+                    if constexpr (FUSED) {
 #pragma unroll
-                    for (int m = 0; m < DPL; m += 4)
-                        *(float4 *) (op + m) = make_float4(o[rt][m][i], o[rt][m + 1][i], o[rt][m + 2][i], o[rt][m + 3][i]);
+                        for (int m = 0; m < DPL; m += 2) store_pair_agent(op + m, o[rt][m][i], o[rt][m + 1][i]);
+                    } else {
+#pragma unroll
+                        for (int m = 0; m < DPL; m += 4)
+                            *(float4 *) (op + m) =
+                                make_float4(o[rt][m][i], o[rt][m + 1][i], o[rt][m + 2][i], o[rt][m + 3][i]);
+                    }
                 }
             }
             const int r = rt * 16 + n;
-            if (g == 0 && r < M) *(float2 *) rec_ml(p, pc.rec, 0, r) = make_float2(m_run[rt], l);
+            if (g == 0 && r < M) {
+                if constexpr (FUSED)
+                    store_pair_agent(rec_ml(p, pc.rec, 0, r), m_run[rt], l);
+                else
+                    *(float2 *) rec_ml(p, pc.rec, 0, r) = make_float2(m_run[rt], l);
+            }
         }
+    }
+    if constexpr (FUSED) {
+        if (pc.pieces > 1 && arrive_last(p.seg_ctr + pc.seg, p.epoch, pc.pieces))
+            for (int row0 = 0; row0 < M; row0 += 16) merge_tile16<D>(p, pc.rec0, pc.pieces, 0, row0, M, w.q0, hk);
     }
 }
 

@@ -14,7 +14,8 @@ hipError_t launch_merge(const AttnParams &p, int head_dim, hipStream_t stream);
 // MFMA prefill kernel (sequences with n_q*gqa > p.decode_rows); grid covers max_query_len*gqa rows.
 hipError_t launch_prefill(const AttnParams &p, int head_dim, int kv_type, int max_rows, hipStream_t stream);
 // A mixed batch over an f16 pool at head size 64 or 128 in one launch: prefill
-// workgroups plus the decode rows' stream-K workers, then the merge.
+// workgroups plus the decode rows' stream-K workers, which merge their split
+// segments themselves.
 hipError_t launch_mixed_f16(const AttnParams &p, int head_dim, int max_rows, hipStream_t stream);
 // The 16-row-tile prefill kernel (pa_prefill16.hip), used at head size 256.
 hipError_t launch_prefill16(const AttnParams &p, int head_dim, int kv_type, int max_rows, hipStream_t stream);

@@ -61,7 +61,9 @@ struct PrefillOcc {
 // decode_piece of pa_decode_body.h) and are dispatched first, one per CU: the
 // HBM-bound decode waves and the MFMA-bound prefill workgroups then share
 // every CU from the start, instead of the decode rows waiting for the prefill
-// tail.  The merge kernel follows on the same stream.
+// tail.  Split decode segments are merged inside the launch (arrive_last):
+// the decode workers finish long before the prefill workgroups, so the merge
+// costs the launch nothing, and the call is one launch.
 template <int D, int NW, int KVT, bool MIXED>
 __global__ __launch_bounds__(NW * 64, PrefillOcc<D>::kWavesPerSimd) void pa_prefill_kernel(AttnParams p, int n_rb,
                                                                                           int n_dec) {
@@ -71,7 +73,7 @@ __global__ __launch_bounds__(NW * 64, PrefillOcc<D>::kWavesPerSimd) void pa_pref
             const int worker = bid * NW + (int) (threadIdx.x >> 6);
             if (worker < p.sk_workers)
                 for_each_piece<false>(p, worker, 0,
-                                      [&](const SeqWindow &w, const Piece &pc) { decode_piece<D, 1>(p, w, pc); });
+                                      [&](const SeqWindow &w, const Piece &pc) { decode_piece<D, 1, true>(p, w, pc); });
             return;
         }
         bid -= n_dec;   // a multiple of 8: the XCD of every prefill workgroup is unchanged
@@ -520,13 +522,11 @@ static hipError_t launch_prefill_kv(const AttnParams &p, int head_dim, int max_r
 }
 
 hipError_t launch_mixed_f16(const AttnParams &p, int head_dim, int max_rows, hipStream_t stream) {
-    hipError_t e;
     switch (head_dim) {
-        case 64: e = launch_prefill_t<64, 4, 1, true>(p, max_rows, stream); break;
-        case 128: e = launch_prefill_t<128, 4, 1, true>(p, max_rows, stream); break;
+        case 64: return launch_prefill_t<64, 4, 1, true>(p, max_rows, stream);
+        case 128: return launch_prefill_t<128, 4, 1, true>(p, max_rows, stream);
         default: return hipErrorInvalidValue;
     }
-    return e != hipSuccess ? e : launch_merge(p, head_dim, stream);
 }
 
 hipError_t launch_prefill(const AttnParams &p, int head_dim, int kv_type, int max_rows, hipStream_t stream) {

@@ -283,15 +283,21 @@ def test_workspace_reuse_across_calls(pa, oracle):
         assert e.max() <= TOL, (it, e.max())
 
 
-@pytest.mark.parametrize("k_type,nq", [(F16, 1), (Q8_0, 5)])
-def test_split_merge_with_garbage_workspace(pa, oracle, k_type, nq):
+# decode kernel (f16; Q8_0 spec-verify) and the mixed prefill launch, whose
+# decode workers merge split segments through tagged counters in the workspace
+SPLIT_CASES = [(F16, (1, 1, 1, 1)), (Q8_0, (5, 5, 5, 5)), (F16, (128, 1, 1, 1))]
+
+
+@pytest.mark.parametrize("k_type,nqs", SPLIT_CASES)
+def test_split_merge_with_garbage_workspace(pa, oracle, k_type, nqs):
     """The workspace needs no initialisation: every record and segment entry
-    the merge reads is written earlier in the same call.  Filled with 0xff,
-    with random bytes, or zeroed, the workspace gives the same bits and the
-    oracle's result."""
-    banner(f"split merge over garbage workspaces k_type={k_type} nq={nq}")
-    rng = np.random.default_rng(48 + nq)
-    c = make_case(rng, 32, 8, 128, [6000, 700, 3000, 2500], [nq] * 4, k_type=k_type, quantize=oracle.quantize_q8_0)
+    the merge reads is written earlier in the same call, and a merge counter
+    holding another call's tag counts as zero.  Filled with 0xff, with random
+    bytes, or zeroed, the workspace gives the same bits (the merging piece
+    reads every record in order) and the oracle's result."""
+    banner(f"split merge over garbage workspaces k_type={k_type} nq={nqs}")
+    rng = np.random.default_rng(48 + sum(nqs))
+    c = make_case(rng, 32, 8, 128, [6000, 700, 3000, 2500], list(nqs), k_type=k_type, quantize=oracle.quantize_q8_0)
     k, v, batch = to_device(pa, c)
     prm = pa.PagedAttnParams(scale=c.scale)
     q = torch.as_tensor(c.q).cuda()
@@ -309,14 +315,15 @@ def test_split_merge_with_garbage_workspace(pa, oracle, k_type, nq):
     assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
 
 
-@pytest.mark.parametrize("k_type,nq", [(F16, 1), (Q8_0, 5)])
-def test_graph_replays_match_eager(pa, oracle, k_type, nq):
-    """A call captured in a graph (decode kernel and merge) and replayed four
-    times, with eager calls of another batch on the same workspace in
-    between, gives the eager call's bits on every replay."""
-    banner(f"graph replays k_type={k_type} nq={nq}")
-    rng = np.random.default_rng(49 + nq)
-    c = make_case(rng, 32, 8, 128, [5000, 700, 3000, 64], [nq] * 4, k_type=k_type, quantize=oracle.quantize_q8_0)
+@pytest.mark.parametrize("k_type,nqs", SPLIT_CASES)
+def test_graph_replays_match_eager(pa, oracle, k_type, nqs):
+    """A call captured in a graph and replayed four times, with eager calls
+    of another batch on the same workspace in between, gives the eager call's
+    bits on every replay (a replay reuses its call's merge-counter tag; the
+    merging piece resets each counter it completes)."""
+    banner(f"graph replays k_type={k_type} nq={nqs}")
+    rng = np.random.default_rng(49 + sum(nqs))
+    c = make_case(rng, 32, 8, 128, [5000, 700, 3000, 2500], list(nqs), k_type=k_type, quantize=oracle.quantize_q8_0)
     k, v, batch = to_device(pa, c)
     prm = pa.PagedAttnParams(scale=c.scale)
     q = torch.as_tensor(c.q).cuda()
