@@ -52,9 +52,49 @@ struct Q8Shape {
     static constexpr int NBL = NB / 2;                      // blocks staged by one lane (2 lanes per cell)
     static constexpr int SH_MAX = (NB == 2) ? 2 : 0;        // lane slices start 4-aligned unless NB == 2
     static constexpr int W = (34 * NBL + SH_MAX + 3) / 4;   // dwords of one lane's load window
-    static constexpr int STRIDE = D * 2 + 16;               // padded LDS row of f16 values (bytes)
+    // LDS rows of f16 values: unpadded with XOR-swizzled chunks at D >= 128
+    // (q8_k_off, q8_v_off), padded by 16 bytes at D = 64
+    static constexpr bool SWZ = D >= 128;
+    static constexpr int STRIDE = SWZ ? D * 2 : D * 2 + 16;
     static constexpr int TILE_BYTES = kTile * STRIDE;
 };
+
+// LDS tile layouts at D >= 128, for 64 banks of 4 bytes: a 16-lane b128
+// access and a 32-lane b64 access each cover one 256-byte bank window, and a
+// row is a whole number of windows.  The staging lanes hold cell l/2, blocks
+// (l%2)*NB/2 .. +NB/2 (q8_load_raw).
+//
+// K: 16-byte chunk c (dims 8c .. 8c+7) of row r sits at chunk
+// c ^ swk(r) ^ (c >= 16 ? 8 : 0).  A QK^T read takes one chunk of rows
+// 8a + b (+4), a, b < 4, over 16 lanes: swk maps them to 16 distinct
+// positions.  A staging write of 16 lanes covers 8 consecutive cells x 2
+// halves of the row, and swk takes 8 distinct values in its low three bits
+// over 8 aligned cells, while the halves differ in bit 3 (chunk + 8 at
+// D = 128; the extra XOR at D = 256, where the halves are 16 chunks apart).
+//
+// V: 32-byte chunk v (dims 16v .. 16v+15) of row r sits at chunk v ^ swv(r),
+// its two 16-byte halves swapped when v >= NB (the chunks the second staging
+// lane of a cell writes).  A transpose read of 32 lanes takes one chunk of
+// rows {0..3, 8..11} + 4i + 16j: swv maps them to 8 distinct positions.  A
+// staging write of 16 lanes (8 cells x 2 lanes, one 16-byte half each) hits
+// 8 distinct chunk positions, and the swap puts the two lanes of a cell in
+// different halves.
+__device__ __forceinline__ int q8_swk(int r) { return (r & 7) ^ (((r >> 3) & 3) << 2); }
+__device__ __forceinline__ int q8_swv(int r) { return (r & 3) | ((((r >> 3) ^ (r >> 2)) & 1) << 2); }
+
+// byte offset of 16-byte K chunk c of row r
+template <int D>
+__device__ __forceinline__ int q8_k_off(int r, int c) {
+    if constexpr (Q8Shape<D>::SWZ) return r * Q8Shape<D>::STRIDE + 16 * (c ^ q8_swk(r) ^ (c >= 16 ? 8 : 0));
+    else return r * Q8Shape<D>::STRIDE + 16 * c;
+}
+// byte offset of byte b (0..31) of 32-byte V chunk v of row r
+template <int D>
+__device__ __forceinline__ int q8_v_off(int r, int v, int b) {
+    if constexpr (Q8Shape<D>::SWZ)
+        return r * Q8Shape<D>::STRIDE + 32 * (v ^ q8_swv(r)) + (v >= Q8Shape<D>::NB ? b ^ 16 : b);
+    else return r * Q8Shape<D>::STRIDE + 32 * v + b;
+}
 
 template <int D>
 struct Q8Lds {
@@ -129,9 +169,11 @@ __device__ __forceinline__ void q8_stage(const uint32_t (&raw)[Q8Shape<D>::W], i
             h[k >> 1][2 * (k & 1)] = lo;
             h[k >> 1][2 * (k & 1) + 1] = hi;
         }
-        char *dst = tile_lds + cell * Q::STRIDE + blk * 64;
 #pragma unroll
-        for (int k = 0; k < 4; k++) *(u32x4 *) (dst + 16 * k) = h[k];
+        for (int k = 0; k < 4; k++) {
+            const int off = DEQ ? q8_v_off<D>(cell, 2 * blk + (k >> 1), 16 * (k & 1)) : q8_k_off<D>(cell, 4 * blk + k);
+            *(u32x4 *) (tile_lds + off) = h[k];
+        }
     }
 }
 
@@ -148,7 +190,7 @@ __device__ __forceinline__ f16x8 lds_tr_b16x8_q8(const char *p0, const char *p1)
 template <int D, int NW>
 __device__ __forceinline__ void q8_piece(const AttnParams &p, Q8Lds<D> &lds, const SeqWindow &w, const Piece &pc) {
     using Q = Q8Shape<D>;
-    constexpr int NB = Q::NB, NPV = D / 16, STRIDE = Q::STRIDE;
+    constexpr int NB = Q::NB, NPV = D / 16;
     constexpr int NRAW = NW == 1 ? 2 : 1;   // pools one wave stages: K and V, or one of them
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
@@ -218,7 +260,7 @@ __device__ __forceinline__ void q8_piece(const AttnParams &p, Q8Lds<D> &lds, con
                 const int cr = 8 * (n >> 2) + 4 * h + (n & 3);
 #pragma unroll
                 for (int ks = 0; ks < NB; ks++) {
-                    const f16x8 a = *(const f16x8 *) (lds.k + cr * STRIDE + (32 * ks + 8 * g) * 2);
+                    const f16x8 a = *(const f16x8 *) (lds.k + q8_k_off<D>(cr, 4 * ks + g));
                     const f32x4 dk = *(const f32x4 *) &lds.ks[ks][8 * g + 4 * h];
                     f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qh[ks], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
                     c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ql[ks], c, 0, 0, 0);
@@ -277,14 +319,15 @@ __device__ __forceinline__ void q8_piece(const AttnParams &p, Q8Lds<D> &lds, con
             l_run += ps;
 
             // O += P V, V staged as f16(q*d)
-            const char *vrow = lds.v + (8 * g + (n >> 2)) * STRIDE + 8 * (n & 3);
+            const int vr = 8 * g + (n >> 2);   // V rows vr, vr + 4 at byte 8(n%4) of chunk m
             const u32x4 pk = {pack_f16x2(pv[0], pv[1]), pack_f16x2(pv[2], pv[3]), pack_f16x2(pv[4], pv[5]),
                               pack_f16x2(pv[6], pv[7])};
             const f16x8 pb = __builtin_bit_cast(f16x8, pk);
             __builtin_amdgcn_s_setprio(1);
 #pragma unroll
             for (int m = 0; m < NPV; m++) {
-                const f16x8 vb = lds_tr_b16x8_q8(vrow + 32 * m, vrow + 4 * STRIDE + 32 * m);
+                const f16x8 vb = lds_tr_b16x8_q8(lds.v + q8_v_off<D>(vr, m, 8 * (n & 3)),
+                                                 lds.v + q8_v_off<D>(vr + 4, m, 8 * (n & 3)));
                 o[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pb, vb, o[m], 0, 0, 0);
             }
             __builtin_amdgcn_s_setprio(0);
