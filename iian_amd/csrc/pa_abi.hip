@@ -18,17 +18,21 @@ using namespace iian_pa;
 
 // Stream-K workers of the decode kernels (for_each_piece, pa_common.h), sized
 // so that every worker's equal share of the call runs at once and the kernel
-// ends with no tail.  The f16 kernel runs one single-wave workgroup per SIMD of
-// a 256-CU MI355X: measured at the Llama-3-8B decode shape, 1024 waves stream
-// the pool faster than 2048 (two per SIMD) or more, and deeper per-wave
-// prefetch gains nothing, so the pool's access pattern, not the number of
-// loads in flight, sets the rate.  The Q8_0 kernel's workers are groups of Hkv
+// ends with no tail.  The f16 kernel runs single-wave workgroups, 1.5 per SIMD
+// of a 256-CU MI355X: measured at the Llama-3-8B decode shape, 1536 waves
+// stream the pool fastest (127.0 us against 127.4 at 1280, 129.2 at 1024,
+// 131.4 at 2048, 131.9 at 1792, 136.4 at 1152), and deeper per-wave prefetch
+// gains nothing, so the pool's access pattern, not the number of loads in
+// flight, sets the rate.  In a mixed launch the decode workers are 1024 waves:
+// each of their workgroups takes a prefill workgroup's slot on its CU while it
+// runs.  The Q8_0 kernel's workers are groups of Hkv
 // workgroups of NW waves over 2048 waves: its LDS staging and conversion want
 // two waves per SIMD (1024 waves measured 1.7x slower at config 4).  At head
 // size 256 a tile moves twice the bytes and 768 waves measured best (Gemma3-12B
 // shapes: sliding-window layer 50.6 us against 56.6 us at 1024, 58.0 at 640,
 // 60.9 at 512, 61.1 at 2048; global layer 808 us against 824 us at 1024).
-constexpr int kF16DecodeWaves = 1024;
+constexpr int kF16DecodeWaves = 1536;
+constexpr int kF16MixedDecodeWaves = 1024;
 constexpr int kF16DecodeWavesD256 = 768;
 constexpr int kQ8DecodeWaves = 2048;
 constexpr int kDecodeWaves = kQ8DecodeWaves > kF16DecodeWaves ? kQ8DecodeWaves : kF16DecodeWaves;
@@ -265,8 +269,10 @@ int iian_pa_attention(void *stream, const float *q, const void *k_pool, const vo
     // prefill workgroups and, after them, the decode rows' stream-K workers,
     // which fill the CUs the MFMA-bound prefill leaves, and merge their split
     // segments themselves.
-    if (type_k == IIAN_PA_TYPE_F16 && head_dim <= 128)
+    if (type_k == IIAN_PA_TYPE_F16 && head_dim <= 128) {
+        p.sk_workers = kF16MixedDecodeWaves;
         return launch_mixed_f16(p, head_dim, max_rows, st) == hipSuccess ? IIAN_PA_OK : IIAN_PA_ERR_HIP;
+    }
 
     // Other mixed batches: the decode rows (HBM-bound) run on a side stream
     // forked from and joined back into the caller's stream, beside the

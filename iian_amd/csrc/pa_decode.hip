@@ -35,9 +35,9 @@
 
 namespace iian_pa {
 
-// One wave per SIMD is launched (kF16DecodeWaves in pa_abi.hip), but the
-// register budget stays at two waves per SIMD up to D*NRT = 128: in a mixed
-// batch these waves share the CUs with the prefill kernel's workgroups.
+// 1.5 waves per SIMD are launched at D <= 128 (kF16DecodeWaves in pa_abi.hip),
+// within a register budget of two waves per SIMD up to D*NRT = 128 (a budget
+// of one wave per SIMD measured slower).
 template <int D, int NRT>
 __global__ __launch_bounds__(64, (D * NRT <= 128) ? 2 : 1) void pa_decode_f16_kernel(AttnParams p) {
     for_each_piece<false>(p, blockIdx.x, 0, [&](const SeqWindow &w, const Piece &pc) { decode_piece<D, NRT>(p, w, pc); });
