@@ -71,9 +71,14 @@ WorkspaceLayout workspace_layout(int32_t n_seqs, int32_t n_head_kv, int32_t head
 // counter (the kernel treats any other tag as a count of zero).
 uint64_t next_epoch() {
     static std::atomic<uint64_t> next{[] {
-        std::random_device rd;
-        const uint64_t t = (uint64_t) std::chrono::steady_clock::now().time_since_epoch().count();
-        return ((uint64_t) rd() << 32 ^ (uint64_t) rd()) ^ t * 0x9e3779b97f4a7c15ull;
+        uint64_t seed = (uint64_t) std::chrono::steady_clock::now().time_since_epoch().count() * 0x9e3779b97f4a7c15ull;
+        seed ^= (uint64_t) (uintptr_t) &seed;
+        try {   // no exception may leave the C ABI; the clock alone still seeds
+            std::random_device rd;
+            seed ^= (uint64_t) rd() << 32 ^ (uint64_t) rd();
+        } catch (...) {
+        }
+        return seed;
     }()};
     return next.fetch_add(1, std::memory_order_relaxed) & ((1ull << 48) - 1);
 }
