@@ -16,36 +16,64 @@ namespace {
 
 using namespace iian_pa;
 
-// Stream-K workers of the decode kernels (for_each_piece, pa_common.h), sized
-// so that every worker's equal share of the call runs at once and the kernel
-// ends with no tail.  The f16 kernel runs single-wave workgroups, 1.5 per SIMD
-// of a 256-CU MI355X: measured at the Llama-3-8B decode shape, 1536 waves
-// stream the pool fastest (127.0 us against 127.4 at 1280, 129.2 at 1024,
-// 131.4 at 2048, 131.9 at 1792, 136.4 at 1152), and deeper per-wave prefetch
-// gains nothing, so the pool's access pattern, not the number of loads in
-// flight, sets the rate.  In a mixed launch the decode workers are 1024 waves:
-// each of their workgroups takes a prefill workgroup's slot on its CU while it
-// runs.  The Q8_0 kernel's workers are groups of Hkv
-// workgroups of NW waves over 2048 waves: its LDS staging and conversion want
-// two waves per SIMD (1024 waves measured 1.7x slower at config 4).  At head
-// size 256 a tile moves twice the bytes and 768 waves measured best (Gemma3-12B
-// shapes: sliding-window layer 50.6 us against 56.6 us at 1024, 58.0 at 640,
-// 60.9 at 512, 61.1 at 2048; global layer 808 us against 824 us at 1024).
-constexpr int kF16DecodeWaves = 1536;
-constexpr int kF16MixedDecodeWaves = 1024;
-constexpr int kF16DecodeWavesD256 = 768;
-constexpr int kQ8DecodeWaves = 2048;
-constexpr int kDecodeWaves = kQ8DecodeWaves > kF16DecodeWaves ? kQ8DecodeWaves : kF16DecodeWaves;
+// Stream-K workers of the decode kernels (for_each_piece, pa_common.h), per CU
+// of the device, sized so that every worker's equal share of the call runs at
+// once and the kernel ends with no tail.  The f16 kernel runs single-wave
+// workgroups, 1.5 per SIMD: measured on a 256-CU MI355X at the Llama-3-8B
+// decode shape, 1536 waves stream the pool fastest (127.0 us against 127.4 at
+// 1280, 129.2 at 1024, 131.4 at 2048, 131.9 at 1792, 136.4 at 1152), and
+// deeper per-wave prefetch gains nothing, so the pool's access pattern, not
+// the number of loads in flight, sets the rate.  In a mixed launch the decode
+// workers are 4 waves per CU: each of their workgroups takes a prefill
+// workgroup's slot on its CU while it runs.  The Q8_0 kernel's workers are
+// groups of Hkv workgroups of NW waves over 8 waves per CU: its LDS staging
+// and conversion want two waves per SIMD (half of that measured 1.7x slower at
+// config 4).  At head size 256 a tile moves twice the bytes and 3 waves per CU
+// measured best (Gemma3-12B shapes: sliding-window layer 50.6 us against 56.6
+// us at 4 per CU, 58.0 at 2.5, 60.9 at 2, 61.1 at 8; global layer 808 us
+// against 824 us at 4 per CU).
+constexpr int kF16DecodeWavesPerCu = 6;
+constexpr int kF16MixedDecodeWavesPerCu = 4;
+constexpr int kF16DecodeWavesPerCuD256 = 3;
+constexpr int kQ8DecodeWavesPerCu = 8;
+constexpr int kMaxWavesPerCu = kQ8DecodeWavesPerCu;
+constexpr int kDefaultCus = 256;   // an MI355X, when the device cannot be queried
+constexpr int kMaxDevices = 64;
+
+// Compute units of device `dev`, queried once per device.
+int device_cus(int dev) {
+    static std::atomic<int> cache[kMaxDevices];
+    if (dev < 0 || dev >= kMaxDevices) return kDefaultCus;
+    int n = cache[dev].load(std::memory_order_relaxed);
+    if (n > 0) return n;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+        n = kDefaultCus;
+    cache[dev].store(n, std::memory_order_relaxed);
+    return n;
+}
+
+int current_device_cus() {
+    int dev = 0;
+    return hipGetDevice(&dev) == hipSuccess ? device_cus(dev) : kDefaultCus;
+}
+
+int stream_device_cus(hipStream_t st) {
+    int dev = 0;
+    if (st != nullptr && hipStreamGetDevice(st, &dev) == hipSuccess) return device_cus(dev);
+    return current_device_cus();
+}
 
 int q8_waves_per_wg(int decode_rows) { return decode_rows > 16 ? 2 : 1; }   // NW of pa_decode_q8_kernel
 
 // Workspace: [partial records (numerators)][(m, l) per record row][segment
 // info][merge counter per (sequence, kv head)], each section 256-byte aligned.  Sized for the record count of
 // either kernel at kDecodeRowsMax rows: the f16 kernel has at most
-// kF16DecodeWaves + S*Hkv one-head records, the Q8_0 kernel at most
-// kQ8DecodeWaves/Hkv + S records of Hkv heads.  A record is padded by 64 floats
+// (f16 workers) + S*Hkv one-head records, the Q8_0 kernel at most
+// (Q8_0 groups) + S records of Hkv heads; both are below
+// kMaxWavesPerCu*CUs + S*Hkv heads.  A record is padded by 64 floats
 // so that consecutive records do not sit at a power-of-two stride (rows at
-// such strides alias onto the same HBM channels).
+// such strides alias onto the same HBM channels).  The general path
+// (pa_general.hip) keeps its split records in the same bytes.
 constexpr int kRecordPad = 64;
 
 struct WorkspaceLayout {
@@ -54,8 +82,8 @@ struct WorkspaceLayout {
 
 inline size_t align256(size_t v) { return (v + 255) & ~(size_t) 255; }
 
-WorkspaceLayout workspace_layout(int32_t n_seqs, int32_t n_head_kv, int32_t head_dim_v) {
-    const size_t rec_heads = (size_t) kDecodeWaves + (size_t) n_seqs * n_head_kv;   // records x heads, upper bound
+WorkspaceLayout workspace_layout(int32_t n_seqs, int32_t n_head_kv, int32_t head_dim_v, int cus) {
+    const size_t rec_heads = (size_t) kMaxWavesPerCu * cus + (size_t) n_seqs * n_head_kv;   // records x heads, upper bound
     WorkspaceLayout l;
     l.o = 0;
     l.ml = l.o + align256((rec_heads * kDecodeRowsMax * head_dim_v + rec_heads * kRecordPad) * sizeof(float));
@@ -90,8 +118,6 @@ struct SideStream {
     hipStream_t stream = nullptr;
     hipEvent_t fork = nullptr, join = nullptr;
 };
-
-constexpr int kMaxDevices = 64;
 
 const SideStream *side_stream_for(hipStream_t caller) {
     int dev = 0;
@@ -129,6 +155,20 @@ int row_bytes(int type, int64_t elems, int64_t &out) {
     }
 }
 
+// The MFMA kernels: K and V both f16 or both Q8_0, head size 64, 128 or 256
+// for both, and a power-of-two block size of at least 8 (the 8-cell groups of
+// a tile must not straddle a block).  Everything else iian_pa_supported
+// accepts runs through the general fp32 kernel.
+bool mfma_path(int type_k, int type_v, int head_dim, int head_dim_v, int bs_log2) {
+    return type_k == type_v && (type_k == IIAN_PA_TYPE_F16 || type_k == IIAN_PA_TYPE_Q8_0) &&
+           head_dim == head_dim_v && (head_dim == 64 || head_dim == 128 || head_dim == 256) && bs_log2 >= 3;
+}
+
+bool head_size_ok(int type, int d) {
+    if (d < 4 || d > 512 || d % 4) return false;
+    return type != IIAN_PA_TYPE_Q8_0 || d % 32 == 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -147,10 +187,9 @@ const char *iian_pa_status_string(int status) {
 
 int iian_pa_supported(int type_k, int type_v, int head_dim, int head_dim_v, float max_alibi_bias) {
     if (max_alibi_bias != 0.0f) return 0;
-    if (type_k != type_v) return 0;
-    if (type_k != IIAN_PA_TYPE_F16 && type_k != IIAN_PA_TYPE_Q8_0) return 0;
-    if (head_dim != head_dim_v) return 0;
-    return head_dim == 64 || head_dim == 128 || head_dim == 256;
+    auto type_ok = [](int t) { return t == IIAN_PA_TYPE_F32 || t == IIAN_PA_TYPE_F16 || t == IIAN_PA_TYPE_Q8_0; };
+    if (!type_ok(type_k) || !type_ok(type_v)) return 0;
+    return head_size_ok(type_k, head_dim) && head_size_ok(type_v, head_dim_v);
 }
 
 int iian_pa_kv_write(void *stream, const float *rows, int64_t n_rows, int64_t row_elems, const int64_t *slots,
@@ -187,29 +226,92 @@ size_t iian_pa_workspace_size(int32_t n_tokens, int32_t n_seqs, int32_t n_head, 
     if (n_tokens < 0 || n_seqs < 0 || n_head <= 0 || n_head_kv <= 0 || head_dim_v <= 0 || max_blocks < 0 ||
         block_size <= 0)
         return 0;
-    return workspace_layout(n_seqs, n_head_kv, head_dim_v).total + 256;   // room to align the caller's base to 256 bytes
+    // + 256: room to align the caller's base to 256 bytes
+    return workspace_layout(n_seqs, n_head_kv, head_dim_v, current_device_cus()).total + 256;
 }
 
-int iian_pa_attention(void *stream, const float *q, const void *k_pool, const void *v_pool, int type_k, int type_v,
-                      int32_t num_blocks, const int32_t *block_tables, int32_t max_blocks, const int32_t *seq_lens,
-                      const int32_t *query_start_loc, const int32_t *pos, int32_t n_tokens, int32_t n_seqs,
-                      int32_t max_query_len, int32_t n_head, int32_t n_head_kv, int32_t head_dim, int32_t head_dim_v,
-                      int32_t block_size, float scale, float softcap, int32_t causal, int32_t n_swa, float *out,
-                      void *workspace, size_t workspace_bytes, int32_t *err_flag) {
+}  // extern "C"
+
+namespace {
+
+// The attention call behind iian_pa_attention, on a workspace of ws_bytes
+// bytes at ws (any alignment; at least workspace_layout(...).total + 256).
+int run_attention(hipStream_t st, const float *q, const void *k_pool, const void *v_pool, int type_k, int type_v,
+                  int32_t num_blocks, const int32_t *block_tables, int32_t max_blocks, const int32_t *seq_lens,
+                  const int32_t *query_start_loc, const int32_t *pos, int32_t n_tokens, int32_t n_seqs,
+                  int32_t max_query_len, int32_t n_head, int32_t n_head_kv, int32_t head_dim, int32_t head_dim_v,
+                  int32_t block_size, float scale, float softcap, int32_t causal, int32_t n_swa, float *out,
+                  void *workspace, size_t workspace_bytes, int32_t *err_flag) {
     if (n_tokens < 0 || n_seqs < 0 || max_query_len < 0) return IIAN_PA_ERR_ARG;
     if (n_tokens == 0 || n_seqs == 0) return IIAN_PA_OK;
     if (!q || !k_pool || !v_pool || !block_tables || !seq_lens || !query_start_loc || !pos || !out)
         return IIAN_PA_ERR_NULL;
     if (n_head <= 0 || n_head_kv <= 0 || n_head % n_head_kv) return IIAN_PA_ERR_ARG;
-    if (num_blocks <= 0 || max_blocks <= 0 || max_query_len == 0 || max_query_len > n_tokens) return IIAN_PA_ERR_ARG;
+    if (num_blocks <= 0 || max_blocks <= 0 || block_size <= 0 || max_query_len == 0 || max_query_len > n_tokens)
+        return IIAN_PA_ERR_ARG;
     if (n_swa < 0 || softcap < 0.0f || !std::isfinite(scale) || !std::isfinite(softcap)) return IIAN_PA_ERR_ARG;
-    const int bs_log2 = log2_exact(block_size);
-    if (bs_log2 < 3) return IIAN_PA_ERR_UNSUPPORTED;   // the 8-cell groups of a tile must not straddle a block
     if (!iian_pa_supported(type_k, type_v, head_dim, head_dim_v, 0.0f)) return IIAN_PA_ERR_UNSUPPORTED;
     if (((uintptr_t) q | (uintptr_t) k_pool | (uintptr_t) v_pool | (uintptr_t) out) & 15) return IIAN_PA_ERR_ARG;
-    const size_t need =
-        iian_pa_workspace_size(n_tokens, n_seqs, n_head, n_head_kv, head_dim_v, max_blocks, block_size);
-    if (!workspace || workspace_bytes < need) return IIAN_PA_ERR_WORKSPACE;
+    const int cus = stream_device_cus(st);
+    const WorkspaceLayout wl = workspace_layout(n_seqs, n_head_kv, head_dim_v, cus);
+    if (!workspace || workspace_bytes < wl.total + 256) return IIAN_PA_ERR_WORKSPACE;
+    char *ws = (char *) (((uintptr_t) workspace + 255) & ~(uintptr_t) 255);
+    int64_t kr, vr;
+    if (row_bytes(type_k, (int64_t) n_head_kv * head_dim, kr) || row_bytes(type_v, (int64_t) n_head_kv * head_dim_v, vr))
+        return IIAN_PA_ERR_ARG;
+    const int bs_log2 = log2_exact(block_size);
+    const int gqa = n_head / n_head_kv;
+
+    if (!mfma_path(type_k, type_v, head_dim, head_dim_v, bs_log2)) {
+        // General fp32 path.  Cell indices within a sequence and pool rows
+        // are int32 / int64 there.
+        if ((int64_t) max_blocks * block_size > INT32_MAX) return IIAN_PA_ERR_UNSUPPORTED;
+        GenParams g = {};
+        g.q = q;
+        g.k_pool = (const char *) k_pool;
+        g.v_pool = (const char *) v_pool;
+        g.bt = block_tables;
+        g.seq_lens = seq_lens;
+        g.qsl = query_start_loc;
+        g.pos = pos;
+        g.out = out;
+        g.err = err_flag;
+        g.k_row = kr;
+        g.v_row = vr;
+        g.max_blocks = max_blocks;
+        g.num_blocks = num_blocks;
+        g.block_size = block_size;
+        g.T = n_tokens;
+        g.S = n_seqs;
+        g.H = n_head;
+        g.Hkv = n_head_kv;
+        g.gqa = gqa;
+        g.D = head_dim;
+        g.Dv = head_dim_v;
+        g.max_q = max_query_len;
+        g.scale = scale;
+        g.softcap = softcap;
+        g.causal = causal ? 1 : 0;
+        g.n_swa = n_swa;
+        g.tile_cells = general_tile_cells(head_dim, head_dim_v);
+        const int rows = general_rows_per_block();
+        g.n_rb = (int) (((int64_t) max_query_len * gqa + rows - 1) / rows);
+        // Split each row block's KV range until the launch holds about 8
+        // workgroups per CU, keeping at least 2 tiles per range of the
+        // longest sequence the tables can hold, and the records inside the
+        // workspace: [T*H][n_split] rows of (Dv floats) + (m, l).
+        const int64_t base = (int64_t) n_seqs * n_head_kv * g.n_rb;
+        const int64_t max_tiles = ((int64_t) max_blocks * block_size + g.tile_cells - 1) / g.tile_cells;
+        int64_t ns = (8LL * cus + base - 1) / base;
+        ns = std::min<int64_t>(ns, std::max<int64_t>(1, max_tiles / 2));
+        ns = std::min<int64_t>(ns, 64);
+        const size_t per_split = (size_t) n_tokens * n_head * (size_t) (head_dim_v + 2) * sizeof(float) + 512;
+        ns = std::min<int64_t>(ns, (int64_t) (wl.total / per_split));
+        g.n_split = (int) std::max<int64_t>(ns, 1);
+        g.part_o = (float *) ws;
+        g.part_ml = (float *) (ws + align256((size_t) n_tokens * n_head * g.n_split * head_dim_v * sizeof(float)));
+        return launch_general(g, type_k, type_v, st) == hipSuccess ? IIAN_PA_OK : IIAN_PA_ERR_HIP;
+    }
 
     AttnParams p = {};
     p.q = q;
@@ -221,9 +323,6 @@ int iian_pa_attention(void *stream, const float *q, const void *k_pool, const vo
     p.pos = pos;
     p.out = out;
     p.err = err_flag;
-    int64_t kr, vr;
-    if (row_bytes(type_k, (int64_t) n_head_kv * head_dim, kr) || row_bytes(type_v, (int64_t) n_head_kv * head_dim_v, vr))
-        return IIAN_PA_ERR_ARG;
     // The kernels index pool rows with 32-bit cell numbers and row lengths
     // (pool_off): 2^32 cells of the smallest supported row (68 bytes, one
     // Q8_0 head of size 64) are 272 GiB, more than an MI355X's 288 GB hold.
@@ -237,7 +336,7 @@ int iian_pa_attention(void *stream, const float *q, const void *k_pool, const vo
     p.S = n_seqs;
     p.H = n_head;
     p.Hkv = n_head_kv;
-    p.gqa = n_head / n_head_kv;
+    p.gqa = gqa;
     p.bs_log2 = bs_log2;
     p.softcap = softcap;
     p.softcap_inv = softcap > 0.0f ? 1.0f / softcap : 0.0f;
@@ -245,6 +344,7 @@ int iian_pa_attention(void *stream, const float *q, const void *k_pool, const vo
     p.qscale = softcap > 0.0f ? scale : scale * kLog2e;
     p.causal = causal ? 1 : 0;
     p.n_swa = n_swa;
+    p.max_q = max_query_len;
     // Row budget of the decode kernel: one 16-row MFMA tile, or two when that
     // covers every sequence of the call (spec-verify); larger sequences go to
     // the prefill kernel.
@@ -253,20 +353,17 @@ int iian_pa_attention(void *stream, const float *q, const void *k_pool, const vo
 
     if (type_k == IIAN_PA_TYPE_Q8_0) {
         p.rec_heads = n_head_kv;
-        p.sk_workers = std::max(1, kQ8DecodeWaves / (q8_waves_per_wg(p.decode_rows) * n_head_kv));
+        p.sk_workers = std::max(1, kQ8DecodeWavesPerCu * cus / (q8_waves_per_wg(p.decode_rows) * n_head_kv));
     } else {
         p.rec_heads = 1;
-        p.sk_workers = head_dim == 256 ? kF16DecodeWavesD256 : kF16DecodeWaves;
+        p.sk_workers = (head_dim == 256 ? kF16DecodeWavesPerCuD256 : kF16DecodeWavesPerCu) * cus;
     }
     p.rec_stride = (int64_t) p.rec_heads * p.decode_rows * head_dim_v + kRecordPad;
-    const WorkspaceLayout wl = workspace_layout(n_seqs, n_head_kv, head_dim_v);
-    char *ws = (char *) (((uintptr_t) workspace + 255) & ~(uintptr_t) 255);
     p.part_o = (float *) (ws + wl.o);
     p.part_ml = (float *) (ws + wl.ml);
     p.seg_info = (int2 *) (ws + wl.seg);
     p.seg_ctr = (uint64_t *) (ws + wl.ctr);
     p.epoch = next_epoch();
-    hipStream_t st = (hipStream_t) stream;
     if (max_rows <= p.decode_rows)
         return launch_decode(p, head_dim, type_k, st) == hipSuccess ? IIAN_PA_OK : IIAN_PA_ERR_HIP;
 
@@ -275,7 +372,7 @@ int iian_pa_attention(void *stream, const float *q, const void *k_pool, const vo
     // which fill the CUs the MFMA-bound prefill leaves, and merge their split
     // segments themselves.
     if (type_k == IIAN_PA_TYPE_F16 && head_dim <= 128) {
-        p.sk_workers = kF16MixedDecodeWaves;
+        p.sk_workers = kF16MixedDecodeWavesPerCu * cus;
         return launch_mixed_f16(p, head_dim, max_rows, st) == hipSuccess ? IIAN_PA_OK : IIAN_PA_ERR_HIP;
     }
 
@@ -294,6 +391,22 @@ int iian_pa_attention(void *stream, const float *q, const void *k_pool, const vo
     if (hipEventRecord(side->join, side->stream) != hipSuccess || hipStreamWaitEvent(st, side->join, 0) != hipSuccess)
         return IIAN_PA_ERR_HIP;
     return ed == hipSuccess ? IIAN_PA_OK : IIAN_PA_ERR_HIP;
+}
+
+}  // namespace
+
+extern "C" {
+
+int iian_pa_attention(void *stream, const float *q, const void *k_pool, const void *v_pool, int type_k, int type_v,
+                      int32_t num_blocks, const int32_t *block_tables, int32_t max_blocks, const int32_t *seq_lens,
+                      const int32_t *query_start_loc, const int32_t *pos, int32_t n_tokens, int32_t n_seqs,
+                      int32_t max_query_len, int32_t n_head, int32_t n_head_kv, int32_t head_dim, int32_t head_dim_v,
+                      int32_t block_size, float scale, float softcap, int32_t causal, int32_t n_swa, float *out,
+                      void *workspace, size_t workspace_bytes, int32_t *err_flag) {
+    return run_attention((hipStream_t) stream, q, k_pool, v_pool, type_k, type_v, num_blocks, block_tables,
+                         max_blocks, seq_lens, query_start_loc, pos, n_tokens, n_seqs, max_query_len, n_head,
+                         n_head_kv, head_dim, head_dim_v, block_size, scale, softcap, causal, n_swa, out, workspace,
+                         workspace_bytes, err_flag);
 }
 
 int iian_pa_dequant_q8_0(void *stream, const void *pool, int64_t n_cells, const int64_t *rows_idx, int64_t n_rows,

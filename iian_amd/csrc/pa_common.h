@@ -50,6 +50,7 @@ struct AttnParams {
     int32_t causal;
     int32_t n_swa;
     int32_t decode_rows;        // sequences with n_q*gqa <= decode_rows use the decode kernel
+    int32_t max_q;              // the caller's max_query_len (a sequence with more tokens sets err bit 2)
     int32_t sk_workers;         // stream-K workers: waves (one kv head each) or groups of Hkv workgroups
     int32_t rec_heads;          // kv heads per partial record: 1, or Hkv for grouped workers
 };
@@ -167,9 +168,18 @@ __device__ __forceinline__ void for_each_piece(const AttnParams &p, int worker, 
     // lanes hold the tile counts of sequences base + lane and their inclusive
     // prefix along the line; a piece's window is re-read with scalar loads
     // (keeping every field in lanes costs registers the tile loop needs)
-    int nt = seq_window(p, lane).nt;
+    SeqWindow w0 = seq_window(p, lane);
+    int nt = w0.nt;
     int total = wave_sum_i(nt);
-    for (int b = 64; b < p.S; b += 64) total += wave_sum_i(seq_window(p, b + lane).nt);
+    bool over = w0.nq > p.max_q;
+    for (int b = 64; b < p.S; b += 64) {
+        const SeqWindow wb = seq_window(p, b + lane);
+        total += wave_sum_i(wb.nt);
+        over |= wb.nq > p.max_q;
+    }
+    // a sequence with more query tokens than the caller's max_query_len may
+    // have rows this launch does not cover: worker 0 flags it (bit 2)
+    if (worker == 0 && __builtin_amdgcn_ballot_w64(over) && lane == 0 && p.err) atomicOr(p.err, 4);
     total = __builtin_amdgcn_readfirstlane(total) * unit;
     const int per = max(kMinPieceTiles, (total + p.sk_workers - 1) / p.sk_workers);
     int start = worker * per;

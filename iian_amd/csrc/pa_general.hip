@@ -1,0 +1,481 @@
+// pa_general.hip - paged attention for every pool-type and head-size combination
+// the MFMA kernels are not built for: F32 pools, mixed K/V types (F32, F16,
+// Q8_0 in any pairing), head sizes 4 .. 512 in steps of 4 (Phi-3's 96, 80,
+// ...), Dv != D, and block sizes that are not a power of two >= 8.
+//
+// The arithmetic is fp32 throughout, as in the reference's Kern<float> and
+// Kern<fp16> (src/iian/paged_attn.cpp:25-87): K and V are widened to fp32 when
+// they are staged (f16 exactly; Q8_0 as q * fp32(d), exactly as
+// dequantize_row_q8_0, ggml-quants.c:553-567), scores are fp32 dot products
+// with the raw fp32 q, scaled after the dot (paged_attn.cpp:126), softcapped
+// as paged_attn.cpp:127, and P and V meet in fp32 FMAs.  F32 pools therefore
+// keep their full precision; nothing is narrowed to f16.
+//
+// Work split.  A workgroup of 4 waves owns 16 query rows of one (sequence,
+// kv head): rows r = j*gqa + g (query token j, head g of the GQA group), 4 per
+// wave, so the group shares every staged K/V tile.  It attends one of the
+// row block's n_split equal ranges of TC-cell tiles (TC = 32, 16 or 8 as the
+// head sizes grow, so a tile stays near 16 KB per tensor).  With n_split = 1
+// the workgroup writes the normalised output rows; otherwise each range
+// writes an unnormalised record (O, m, l) per row and pa_general_merge_kernel
+// combines them with a log-sum-exp merge.
+//
+// Per tile: the rows of its TC cells are looked up once through the block
+// table (any block size: cell = table[i / bs] * bs + i % bs,
+// include/iian/kv_cache.h:135-137); every thread loads its quads (4
+// consecutive elements) of the next tile into registers while the current
+// tile is computed from LDS, then widens them to fp32 into LDS.
+//
+//   S = Q K^T   lane (c, j) of a wave: cell c of the tile, dims 4j, 4j + 4P,
+//               ... (P = 64/TC lanes per cell), for the wave's 4 rows; the P
+//               partial sums are added with xor shuffles
+//   softmax     online, exp2 domain, per row; masks as paged_attn.cpp:124
+//   O += P V    lane owns output dims 4l .. 4l+3 (and 256 + 4l ..) of the
+//               wave's 4 rows; P comes from LDS as one broadcast float4 per
+//               cell
+//
+// Semantics: paged_attn_impl (src/iian/paged_attn.cpp:90-146), all-masked rows
+// -> zeros (:132).
+#include "pa_common.h"
+#include "pa_launch.h"
+
+namespace iian_pa {
+
+namespace {
+
+constexpr int kGenWaves = 4;
+constexpr int kGenRowsPerWave = 4;
+constexpr int kGenRows = kGenWaves * kGenRowsPerWave;
+constexpr int kGenMaxTile = 32;
+
+// Raw bytes of 4 consecutive elements e .. e+3 (e % 4 == 0) of head slice
+// `head` of pool row `row`; zeros for row < 0 (a cell beyond the sequence,
+// which must stage as 0 so that P = 0 never meets a non-finite V).
+template <int TY>
+__device__ __forceinline__ u32x4 gen_load(const char *pool, int64_t row, int64_t row_bytes, int head, int dim,
+                                          int e) {
+    u32x4 r = {0u, 0u, 0u, 0u};
+    if (row < 0) return r;
+    const char *base = pool + row * row_bytes;
+    if constexpr (TY == 0) {
+        r = *(const u32x4 *) (base + ((int64_t) head * dim + e) * 4);
+    } else if constexpr (TY == 1) {
+        const u32x2 x = *(const u32x2 *) (base + ((int64_t) head * dim + e) * 2);
+        r[0] = x[0];
+        r[1] = x[1];
+    } else {
+        // Q8_0: block e/32 of the head slice is {f16 d, int8 q[32]} (ggml-common.h:251-256);
+        // the 4 quants sit 2-byte aligned at 2 + e%32
+        const char *blk = base + (int64_t) head * (dim / 32) * 34 + 34 * (e >> 5);
+        const uint16_t *qp = (const uint16_t *) (blk + 2 + (e & 31));
+        r[0] = (uint32_t) qp[0] | ((uint32_t) qp[1] << 16);
+        r[1] = *(const uint16_t *) blk;
+    }
+    return r;
+}
+
+// fp32 values of a quad from gen_load: exact widening (f16), q * fp32(d) (Q8_0).
+template <int TY>
+__device__ __forceinline__ float4 gen_widen(const u32x4 &r) {
+    if constexpr (TY == 0) {
+        return make_float4(__uint_as_float(r[0]), __uint_as_float(r[1]), __uint_as_float(r[2]),
+                           __uint_as_float(r[3]));
+    } else if constexpr (TY == 1) {
+        const _Float16 a = __builtin_bit_cast(_Float16, (uint16_t) r[0]);
+        const _Float16 b = __builtin_bit_cast(_Float16, (uint16_t) (r[0] >> 16));
+        const _Float16 c = __builtin_bit_cast(_Float16, (uint16_t) r[1]);
+        const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t) (r[1] >> 16));
+        return make_float4((float) a, (float) b, (float) c, (float) d);
+    } else {
+        const float d = (float) __builtin_bit_cast(_Float16, (uint16_t) r[1]);
+        return make_float4((float) (int8_t) (r[0]) * d, (float) (int8_t) (r[0] >> 8) * d,
+                           (float) (int8_t) (r[0] >> 16) * d, (float) (int8_t) (r[0] >> 24) * d);
+    }
+}
+
+__device__ __forceinline__ float gen_row_sum(float v, int tc) {
+    for (int o = 1; o < tc; o <<= 1) v += __shfl_xor(v, o);
+    return v;
+}
+__device__ __forceinline__ float gen_row_max(float v, int tc) {
+    for (int o = 1; o < tc; o <<= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+}  // namespace
+
+// Dynamic LDS: K tile [TC][D+4] f32 | V tile [TC][Dv+4] f32 | q [16][D] f32 |
+// P [4 waves][TC][4 rows] f32.  The +4 pad spreads the cells of a QK^T read
+// over the banks.
+template <int KT, int VT>
+__global__ __launch_bounds__(kGenWaves * 64) void pa_general_kernel(GenParams p) {
+    extern __shared__ __attribute__((aligned(16))) float gen_lds[];
+    __shared__ int64_t rows_lds[2][kGenMaxTile];
+
+    const int TC = p.tile_cells, D = p.D, Dv = p.Dv;
+    const int kst = D + 4, vst = Dv + 4;
+    float *Kl = gen_lds;
+    float *Vl = Kl + TC * kst;
+    float *Ql = Vl + TC * vst;
+    float *Pl = Ql + kGenRows * D;
+
+    // workgroup -> (pair, row block, split); the splits of one row block are
+    // neighbours, and so are the row blocks of one (sequence, kv head)
+    const int64_t wid = blockIdx.x;
+    const int z = (int) (wid % p.n_split);
+    const int64_t rest = wid / p.n_split;
+    const int rb = (int) (rest % p.n_rb);
+    const int pair = (int) (rest / p.n_rb);
+    const int s = pair / p.Hkv, hk = pair % p.Hkv;
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int L = max(p.seq_lens[s], 0);
+    const int q0 = min(max(p.qsl[s], 0), p.T);
+    const int nq = min(max(p.qsl[s + 1], q0), p.T) - q0;
+    const int M = nq * p.gqa;
+    // a sequence with more query tokens than the caller's max_query_len has
+    // rows no workgroup of this launch covers: flag it (bit 2)
+    if (rb == 0 && z == 0 && hk == 0 && tid == 0 && nq > p.max_q && p.err) atomicOr(p.err, 4);
+    const int R0 = rb * kGenRows;
+    if (R0 >= M) return;
+
+    // positions of the workgroup's rows and of this wave's rows
+    int wg_min = INT32_MAX, wg_max = INT32_MIN;
+    {
+        const int j0 = R0 / p.gqa, j1 = (min(M, R0 + kGenRows) - 1) / p.gqa;
+        for (int j = j0 + lane; j <= j1; j += 64) {
+            const int ps = p.pos[q0 + j];
+            wg_min = min(wg_min, ps);
+            wg_max = max(wg_max, ps);
+        }
+        for (int o = 32; o >= 1; o >>= 1) {
+            wg_min = min(wg_min, __shfl_xor(wg_min, o));
+            wg_max = max(wg_max, __shfl_xor(wg_max, o));
+        }
+    }
+    int prow[kGenRowsPerWave];
+    bool rlive[kGenRowsPerWave];
+    int w_min = INT32_MAX, w_max = INT32_MIN;
+#pragma unroll
+    for (int i = 0; i < kGenRowsPerWave; i++) {
+        const int r = R0 + wave * kGenRowsPerWave + i;
+        rlive[i] = r < M;
+        prow[i] = rlive[i] ? p.pos[q0 + r / p.gqa] : 0;
+        if (rlive[i]) {
+            w_min = min(w_min, prow[i]);
+            w_max = max(w_max, prow[i]);
+        }
+    }
+    const bool wave_live = rlive[0];
+
+    // the cells any row of the workgroup can see, and this split's tiles of them
+    int c_hi = L;
+    if (p.causal) c_hi = min(c_hi, max(wg_max + 1, 0));
+    const int c_lo = p.n_swa > 0 ? min(max(0, wg_min - p.n_swa + 1), c_hi) : 0;
+    const int nt = (c_hi - c_lo + TC - 1) / TC;
+    const int per = (nt + p.n_split - 1) / p.n_split;
+    const int t0 = min(nt, z * per), t1 = min(nt, t0 + per);
+
+    // q rows of the workgroup into LDS (raw fp32; the scale follows the dot)
+    const int dq = D >> 2;
+    for (int i = tid; i < kGenRows * dq; i += kGenWaves * 64) {
+        const int r = i / dq, c4 = i - r * dq;
+        const int rr = R0 + r;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (rr < M) {
+            const int t = q0 + rr / p.gqa, h = hk * p.gqa + rr % p.gqa;
+            v = *(const float4 *) (p.q + ((int64_t) t * p.H + h) * D + 4 * c4);
+        }
+        *(float4 *) (Ql + r * D + 4 * c4) = v;
+    }
+
+    // pool rows of the TC cells of tile t (by threads 0 .. TC-1)
+    auto tile_rows = [&](int t, int buf) {
+        if (tid < TC) {
+            const int c = c_lo + t * TC + tid;
+            int64_t row = -1;
+            if (c < c_hi) {
+                int b = c / p.block_size;
+                if (b >= p.max_blocks) {
+                    if (p.err) atomicOr(p.err, 2);
+                    b = p.max_blocks - 1;
+                }
+                int32_t id = p.bt[(int64_t) s * p.max_blocks + b];
+                if ((uint32_t) id >= (uint32_t) p.num_blocks) {
+                    if (p.err) atomicOr(p.err, 2);
+                    id = 0;
+                }
+                row = (int64_t) id * p.block_size + (c - b * p.block_size);
+                if (c - b * p.block_size >= p.block_size) row = (int64_t) id * p.block_size;   // clamped b
+            }
+            rows_lds[buf][tid] = row;
+        }
+    };
+
+    // per-thread quads of one tile: K quads i = tid + 256k of TC*D/4, V likewise
+    const int kq = TC * dq, vq = TC * (Dv >> 2);
+    u32x4 kraw[4], vraw[4];
+    auto load_tile = [&](int buf) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int i = tid + k * kGenWaves * 64;
+            if (i < kq) {
+                const int c = i / dq, e = 4 * (i - c * dq);
+                kraw[k] = gen_load<KT>(p.k_pool, rows_lds[buf][c], p.k_row, hk, D, e);
+            }
+            if (i < vq) {
+                const int c = i / (Dv >> 2), e = 4 * (i - c * (Dv >> 2));
+                vraw[k] = gen_load<VT>(p.v_pool, rows_lds[buf][c], p.v_row, hk, Dv, e);
+            }
+        }
+    };
+    auto store_tile = [&]() {
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int i = tid + k * kGenWaves * 64;
+            if (i < kq) {
+                const int c = i / dq, e = 4 * (i - c * dq);
+                *(float4 *) (Kl + c * kst + e) = gen_widen<KT>(kraw[k]);
+            }
+            if (i < vq) {
+                const int c = i / (Dv >> 2), e = 4 * (i - c * (Dv >> 2));
+                *(float4 *) (Vl + c * vst + e) = gen_widen<VT>(vraw[k]);
+            }
+        }
+    };
+
+    const int P = 64 / TC;                 // lanes per cell in QK^T
+    const int cl = lane % TC, jl = lane / TC;
+    const int ndv = Dv >> 2;               // output quads per row
+    float m_run[kGenRowsPerWave], l_run[kGenRowsPerWave];
+    float4 o[kGenRowsPerWave][2];
+#pragma unroll
+    for (int i = 0; i < kGenRowsPerWave; i++) {
+        m_run[i] = -INFINITY;
+        l_run[i] = 0.f;
+        o[i][0] = o[i][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    float *Pw = Pl + wave * TC * 4;
+
+    auto compute = [&](int t) {
+        const int base = c_lo + t * TC;
+        if (!wave_live) return;
+        if (p.causal && base > w_max) return;                          // after every row of the wave
+        if (p.n_swa > 0 && base + TC - 1 <= w_min - p.n_swa) return;   // out of every row's window
+        // scores of cell cl for the wave's rows
+        float acc[kGenRowsPerWave] = {0.f, 0.f, 0.f, 0.f};
+        const float *kr = Kl + cl * kst;
+        const float *qr = Ql + wave * kGenRowsPerWave * D;
+        for (int d = 4 * jl; d < D; d += 4 * P) {
+            const float4 k4 = *(const float4 *) (kr + d);
+#pragma unroll
+            for (int i = 0; i < kGenRowsPerWave; i++) {
+                const float4 q4 = *(const float4 *) (qr + i * D + d);
+                acc[i] = fmaf(q4.x, k4.x, acc[i]);
+                acc[i] = fmaf(q4.y, k4.y, acc[i]);
+                acc[i] = fmaf(q4.z, k4.z, acc[i]);
+                acc[i] = fmaf(q4.w, k4.w, acc[i]);
+            }
+        }
+        const int c = base + cl;
+        float pv[kGenRowsPerWave], alpha[kGenRowsPerWave];
+#pragma unroll
+        for (int i = 0; i < kGenRowsPerWave; i++) {
+            for (int off = TC; off < 64; off <<= 1) acc[i] += __shfl_xor(acc[i], off);
+            float sc = acc[i] * p.scale;
+            if (p.softcap > 0.f) sc = p.softcap * tanhf(sc / p.softcap);
+            const bool vis = rlive[i] && c < c_hi && (!p.causal || c <= prow[i]) &&
+                             (p.n_swa <= 0 || prow[i] - c < p.n_swa);
+            const float x = vis ? sc * kLog2e : -INFINITY;
+            const float mt = gen_row_max(x, TC);
+            const float mnew = fmaxf(m_run[i], mt);
+            if (mnew == -INFINITY) {
+                alpha[i] = 1.f;
+                pv[i] = 0.f;
+            } else {
+                alpha[i] = __builtin_amdgcn_exp2f(m_run[i] - mnew);
+                pv[i] = __builtin_amdgcn_exp2f(x - mnew);
+            }
+            m_run[i] = mnew;
+            l_run[i] = l_run[i] * alpha[i] + gen_row_sum(pv[i], TC);
+        }
+        if (jl == 0) *(float4 *) (Pw + 4 * cl) = make_float4(pv[0], pv[1], pv[2], pv[3]);
+        lds_barrier<1>();   // this wave's P stores before its reads (no s_barrier)
+#pragma unroll
+        for (int i = 0; i < kGenRowsPerWave; i++) {
+            o[i][0].x *= alpha[i]; o[i][0].y *= alpha[i]; o[i][0].z *= alpha[i]; o[i][0].w *= alpha[i];
+            o[i][1].x *= alpha[i]; o[i][1].y *= alpha[i]; o[i][1].z *= alpha[i]; o[i][1].w *= alpha[i];
+        }
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const int d4 = lane + 64 * k;
+            if (d4 >= ndv) break;
+            const float *vc = Vl + 4 * d4;
+            for (int cc = 0; cc < TC; cc++) {
+                const float4 v4 = *(const float4 *) (vc + cc * vst);
+                const float4 pp = *(const float4 *) (Pw + 4 * cc);
+                const float pr[4] = {pp.x, pp.y, pp.z, pp.w};
+#pragma unroll
+                for (int i = 0; i < kGenRowsPerWave; i++) {
+                    o[i][k].x = fmaf(pr[i], v4.x, o[i][k].x);
+                    o[i][k].y = fmaf(pr[i], v4.y, o[i][k].y);
+                    o[i][k].z = fmaf(pr[i], v4.z, o[i][k].z);
+                    o[i][k].w = fmaf(pr[i], v4.w, o[i][k].w);
+                }
+            }
+        }
+        lds_barrier<1>();   // P reads done before the next tile's P stores
+    };
+
+    if (t0 < t1) {
+        tile_rows(t0, 0);
+        __syncthreads();
+        load_tile(0);
+        for (int t = t0; t < t1; t++) {
+            const int buf = (t - t0) & 1;
+            __syncthreads();   // every wave is done with the K/V tile in LDS
+            store_tile();
+            if (t + 1 < t1) tile_rows(t + 1, buf ^ 1);
+            __syncthreads();
+            if (t + 1 < t1) load_tile(buf ^ 1);
+            compute(t);
+        }
+    }
+
+    if (!wave_live) return;
+#pragma unroll
+    for (int i = 0; i < kGenRowsPerWave; i++) {
+        if (!rlive[i]) continue;
+        const int r = R0 + wave * kGenRowsPerWave + i;
+        const int t = q0 + r / p.gqa, h = hk * p.gqa + r % p.gqa;
+        const int64_t orow = (int64_t) t * p.H + h;
+        if (p.n_split == 1) {
+            const float inv = l_run[i] > 0.f ? 1.f / l_run[i] : 0.f;
+#pragma unroll
+            for (int k = 0; k < 2; k++) {
+                const int d4 = lane + 64 * k;
+                if (d4 < ndv)
+                    *(float4 *) (p.out + orow * Dv + 4 * d4) =
+                        make_float4(o[i][k].x * inv, o[i][k].y * inv, o[i][k].z * inv, o[i][k].w * inv);
+            }
+        } else {
+            const int64_t rec = orow * p.n_split + z;
+#pragma unroll
+            for (int k = 0; k < 2; k++) {
+                const int d4 = lane + 64 * k;
+                if (d4 < ndv) *(float4 *) (p.part_o + rec * Dv + 4 * d4) = o[i][k];
+            }
+            if (lane == 0) *(float2 *) (p.part_ml + 2 * rec) = make_float2(m_run[i], l_run[i]);
+        }
+    }
+}
+
+// Log-sum-exp merge of the n_split records of every output row (one wave per
+// row): out = sum_j 2^(m_j - m) O_j / sum_j 2^(m_j - m) l_j, m = max_j m_j.  A
+// record with m_j = -inf (a range with no visible cell, or no tile at all) is
+// skipped, so its O is never read.
+__global__ __launch_bounds__(256) void pa_general_merge_kernel(GenParams p) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t row = (int64_t) blockIdx.x * 4 + wave;
+    if (row >= (int64_t) p.T * p.H) return;
+    const int ns = p.n_split;
+    // rows of a sequence past the launch's row blocks have no records
+    const int t = (int) (row / p.H), h = (int) (row % p.H);
+    int s = 0;
+    {
+        int lo = 0, hi = p.S - 1;   // last s with qsl[s] <= t
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (p.qsl[mid] <= t) lo = mid; else hi = mid - 1;
+        }
+        s = lo;
+    }
+    const int j = t - p.qsl[s];
+    if (j < 0 || (j * p.gqa + h % p.gqa) >= p.n_rb * kGenRows) return;
+    const float2 ml = lane < ns ? *(const float2 *) (p.part_ml + 2 * (row * ns + lane)) : make_float2(-INFINITY, 0.f);
+    const float mx = wave_max(gen_row_max(ml.x, 16));
+    const int ndv = p.Dv >> 2;
+    float4 acc[2] = {make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f)};
+    float lsum = 0.f;
+    if (mx != -INFINITY) {
+        const float w = ml.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml.x - mx);
+        lsum = w * ml.y;
+        for (int o = 1; o < 64; o <<= 1) lsum += __shfl_xor(lsum, o);
+        for (int r = 0; r < ns; r++) {
+            const float wr = __shfl(w, r);
+            if (wr == 0.f) continue;   // wave-uniform
+            const float *op = p.part_o + (row * ns + r) * p.Dv;
+#pragma unroll
+            for (int k = 0; k < 2; k++) {
+                const int d4 = lane + 64 * k;
+                if (d4 < ndv) {
+                    const float4 v = *(const float4 *) (op + 4 * d4);
+                    acc[k].x = fmaf(wr, v.x, acc[k].x);
+                    acc[k].y = fmaf(wr, v.y, acc[k].y);
+                    acc[k].z = fmaf(wr, v.z, acc[k].z);
+                    acc[k].w = fmaf(wr, v.w, acc[k].w);
+                }
+            }
+        }
+    }
+    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const int d4 = lane + 64 * k;
+        if (d4 < ndv)
+            *(float4 *) (p.out + row * p.Dv + 4 * d4) =
+                make_float4(acc[k].x * inv, acc[k].y * inv, acc[k].z * inv, acc[k].w * inv);
+    }
+}
+
+size_t general_lds_bytes(int tile_cells, int D, int Dv) {
+    return ((size_t) tile_cells * (D + 4) + (size_t) tile_cells * (Dv + 4) + (size_t) kGenRows * D +
+            (size_t) kGenWaves * tile_cells * 4) *
+           sizeof(float);
+}
+
+int general_tile_cells(int D, int Dv) {
+    const int m = D > Dv ? D : Dv;
+    return m <= 128 ? 32 : (m <= 256 ? 16 : 8);
+}
+
+int general_rows_per_block() { return kGenRows; }
+
+template <int KT, int VT>
+static hipError_t launch_general_t(const GenParams &p, hipStream_t stream) {
+    const size_t lds = general_lds_bytes(p.tile_cells, p.D, p.Dv);
+    const int64_t nwg = (int64_t) p.S * p.Hkv * p.n_rb * p.n_split;
+    if (nwg <= 0 || nwg > INT32_MAX) return hipErrorInvalidValue;
+    if (lds > 64 * 1024) {   // head sizes above 256: more than 64 KB of dynamic LDS needs the opt-in
+        const hipError_t e = hipFuncSetAttribute((const void *) pa_general_kernel<KT, VT>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL((pa_general_kernel<KT, VT>), dim3((unsigned) nwg), dim3(kGenWaves * 64), lds, stream, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || p.n_split == 1) return e;
+    const int64_t rows = (int64_t) p.T * p.H;
+    hipLaunchKernelGGL(pa_general_merge_kernel, dim3((unsigned) ((rows + 3) / 4)), dim3(256), 0, stream, p);
+    return hipGetLastError();
+}
+
+template <int KT>
+static hipError_t launch_general_k(const GenParams &p, int type_v, hipStream_t stream) {
+    switch (type_v) {
+        case 0: return launch_general_t<KT, 0>(p, stream);
+        case 1: return launch_general_t<KT, 1>(p, stream);
+        case 8: return launch_general_t<KT, 8>(p, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_general(const GenParams &p, int type_k, int type_v, hipStream_t stream) {
+    switch (type_k) {
+        case 0: return launch_general_k<0>(p, type_v, stream);
+        case 1: return launch_general_k<1>(p, type_v, stream);
+        case 8: return launch_general_k<8>(p, type_v, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace iian_pa

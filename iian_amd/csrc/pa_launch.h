@@ -5,6 +5,30 @@
 
 namespace iian_pa {
 
+// Everything the general fp32 kernel (pa_general.hip) reads, by value.
+struct GenParams {
+    const float *q;             // [T][H][D]
+    const char *k_pool;         // cell rows of Hkv*D elements of the K type
+    const char *v_pool;         // cell rows of Hkv*Dv elements of the V type
+    const int32_t *bt;          // [S][max_blocks]
+    const int32_t *seq_lens;    // [S]
+    const int32_t *qsl;         // [S+1]
+    const int32_t *pos;         // [T]
+    float *out;                 // [T][H][Dv]
+    float *part_o;              // split records: [T*H][n_split][Dv]
+    float *part_ml;             // [T*H][n_split] of (m in log2 units, l)
+    int32_t *err;               // nullable error word
+    int64_t k_row, v_row;       // bytes per pool row
+    int32_t max_blocks, num_blocks, block_size;
+    int32_t T, S, H, Hkv, gqa, D, Dv;
+    int32_t max_q;              // the caller's max_query_len
+    int32_t n_rb;               // 16-row blocks launched per (sequence, kv head)
+    int32_t n_split;            // KV ranges per row block (1 .. 64)
+    int32_t tile_cells;         // TC: 32, 16 or 8
+    float scale, softcap;
+    int32_t causal, n_swa;
+};
+
 // Decode / spec-verify kernel (sequences with n_q*gqa <= p.decode_rows) plus the stream-K merge.
 hipError_t launch_decode(const AttnParams &p, int head_dim, int kv_type, hipStream_t stream);
 // The Q8_0-pool variant of launch_decode (pa_decode_q8.hip).
@@ -19,6 +43,13 @@ hipError_t launch_prefill(const AttnParams &p, int head_dim, int kv_type, int ma
 hipError_t launch_mixed_f16(const AttnParams &p, int head_dim, int max_rows, hipStream_t stream);
 // The 16-row-tile prefill kernel (pa_prefill16.hip), used at head size 256.
 hipError_t launch_prefill16(const AttnParams &p, int head_dim, int kv_type, int max_rows, hipStream_t stream);
+
+// General fp32 path (pa_general.hip): any K/V types of F32, F16, Q8_0; head
+// sizes 4..512 in steps of 4; any block size.
+hipError_t launch_general(const GenParams &p, int type_k, int type_v, hipStream_t stream);
+size_t general_lds_bytes(int tile_cells, int D, int Dv);
+int general_tile_cells(int D, int Dv);
+int general_rows_per_block();
 
 hipError_t launch_kv_write(const float *rows, int64_t n_rows, int64_t row_elems, const int64_t *slots, void *pool,
                            int64_t n_cells, int type, int32_t *err, hipStream_t stream);

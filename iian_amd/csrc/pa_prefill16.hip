@@ -94,6 +94,9 @@ __global__ __launch_bounds__(NW * 64, (D == 128 && KVT == 1) ? 4 : (D <= 128 ? 2
     const int q0 = min(max(p.qsl[s], 0), p.T);
     const int nq = min(max(p.qsl[s + 1], q0), p.T) - q0;
     const int M = nq * p.gqa;
+    // more query tokens than the caller's max_query_len: rows past this
+    // launch's row blocks stay unwritten, so flag it (bit 2)
+    if (rb == 0 && hk == 0 && tid == 0 && nq > p.max_q && p.err) atomicOr(p.err, 4);
     if (M <= p.decode_rows) return;
     const int R0 = rb * ROWS;
     if (R0 >= M) return;

@@ -215,6 +215,23 @@ def new_workspace(n_tokens: int, n_seqs: int, n_head: int, n_head_kv: int, head_
     return torch.empty(n, dtype=torch.uint8, device=device)
 
 
+def _check_batch(batch: PagedBatch, device: torch.device) -> None:
+    """The batch arrays are read by the kernels as contiguous int32 (int64
+    for slots) device arrays of the documented shapes: anything else would be
+    misread, so it is rejected here."""
+    S = batch.n_seqs
+    want = (("block_tables", torch.int32, 2), ("seq_lens", torch.int32, 1), ("query_start_loc", torch.int32, 1),
+            ("pos", torch.int32, 1))
+    for name, dt, nd in want:
+        t = getattr(batch, name)
+        if t.dtype != dt or t.dim() != nd or not t.is_contiguous() or t.device != device:
+            raise ValueError(f"batch.{name} must be a contiguous {dt} {nd}-d tensor on {device}")
+    if batch.query_start_loc.shape[0] != S + 1:
+        raise ValueError("batch.query_start_loc must have n_seqs + 1 entries")
+    if batch.block_tables.shape[0] != S:
+        raise ValueError("batch.block_tables must have one row per sequence")
+
+
 def build_paged_attn(q: torch.Tensor, k_cache: KVPool, v_cache: KVPool, n_head_kv: int,
                      params: PagedAttnParams, batch: PagedBatch, out: Optional[torch.Tensor] = None,
                      workspace: Optional[torch.Tensor] = None,
@@ -232,13 +249,24 @@ def build_paged_attn(q: torch.Tensor, k_cache: KVPool, v_cache: KVPool, n_head_k
     if k_cache.n_embd // n_head_kv != D:
         raise ValueError("k head size differs from q head size")
     Dv = v_cache.n_embd // n_head_kv
+    if not q.is_cuda:
+        raise ValueError("q must be a GPU tensor")
     if T != batch.n_tokens:
         raise ValueError("q and batch disagree on n_tokens")
+    _check_batch(batch, q.device)
+    for pool in (k_cache, v_cache):
+        if pool.data.device != q.device:
+            raise ValueError("pools must be on q's device")
     if k_cache.n_cells != v_cache.n_cells or k_cache.n_cells % batch.block_size:
         raise ValueError("pools must hold the same whole number of blocks")
     num_blocks = k_cache.n_cells // batch.block_size
     if out is None:
         out = torch.empty((T, H, Dv), dtype=torch.float32, device=q.device)
+    elif (out.dtype != torch.float32 or tuple(out.shape) != (T, H, Dv) or out.device != q.device
+          or not out.is_contiguous()):
+        raise ValueError(f"out must be a contiguous f32 [{T}, {H}, {Dv}] tensor on q's device")
+    if err_flag is not None and (err_flag.dtype != torch.int32 or err_flag.device != q.device or err_flag.numel() < 1):
+        raise ValueError("err_flag must be an int32 tensor on q's device")
     max_blocks = int(batch.block_tables.shape[1])
     need = workspace_size(T, batch.n_seqs, H, n_head_kv, Dv, max_blocks, batch.block_size)
     if workspace is None:

@@ -49,11 +49,18 @@ enum { IIAN_PA_TYPE_F32 = 0, IIAN_PA_TYPE_F16 = 1, IIAN_PA_TYPE_Q8_0 = 8 };
 /* Human-readable text of a status code (static storage). */
 const char *iian_pa_status_string(int status);
 
-/* Replaces paged_attn_supported (src/iian/paged_attn.cpp:15-18), widened to
- * Q8_0 and to the head sizes the kernels are built for.  Returns 1 when
- * iian_pa_attention accepts this combination, else 0.  K and V must have the
- * same type (F16 or Q8_0), head_dim == head_dim_v in {64, 128, 256}, and no
- * ALiBi (max_alibi_bias == 0). */
+/* Replaces paged_attn_supported (src/iian/paged_attn.cpp:15-18).  Returns 1
+ * when iian_pa_attention accepts this combination, else 0.  Accepted: no
+ * ALiBi (max_alibi_bias == 0), K and V each F32, F16 or Q8_0 in any pairing
+ * (the reference's four F16/F32 pairings, paged_attn.cpp:148-155, widened to
+ * Q8_0), and head sizes head_dim (K) and head_dim_v (V, which may differ,
+ * paged_attn.cpp:163) that are multiples of 4 in [4, 512], multiples of 32
+ * for a Q8_0 pool.  The reference accepts any head size; sizes outside that
+ * set are the documented remainder and return 0.
+ * Both f16 or both Q8_0 at head size 64, 128 or 256 with a power-of-two block
+ * size >= 8 run on the MFMA kernels; every other accepted combination runs on
+ * the general fp32 kernel (fp32 arithmetic throughout, F32 pools keep full
+ * precision). */
 int iian_pa_supported(int type_k, int type_v, int head_dim, int head_dim_v, float max_alibi_bias);
 
 /* Replaces ggml_set_rows(cache, rows, slots) on the K or V pool
@@ -81,9 +88,11 @@ int iian_pa_kv_write_kv(void *stream, const float *k_rows, const float *v_rows, 
                         void *k_pool, void *v_pool, int64_t n_cells, int type_k, int type_v,
                         int32_t *err_flag);
 
-/* Bytes of device workspace iian_pa_attention needs for these sizes (stream-K
- * partial records of the decode rows; the size depends on n_seqs, n_head_kv
- * and head_dim_v only).  Returns 0 on invalid arguments.  No counterpart in the
+/* Bytes of device workspace iian_pa_attention needs for these sizes on the
+ * current device (stream-K partial records of the decode rows, or the split
+ * records of the general kernel; the size depends on n_seqs, n_head_kv,
+ * head_dim_v and the device's compute-unit count only).  Returns 0 on invalid
+ * arguments.  No counterpart in the
  * reference, whose CPU op keeps its scratch in thread_local vectors
  * (src/iian/paged_attn.cpp:108-110).  The workspace needs no initialisation and
  * can be reused by later calls on the same stream; concurrent calls (different
@@ -114,8 +123,12 @@ size_t iian_pa_workspace_size(int32_t n_tokens, int32_t n_seqs, int32_t n_head, 
  *   max_query_len   host int: max tokens of one sequence in this call
  *   out             f32 [T][H][Dv]
  *   workspace       device scratch of at least iian_pa_workspace_size(...) bytes
- * Block ids outside [0, num_blocks) are clamped (never dereferenced out of the
- * pool) and set bit 1 of *err_flag when err_flag is non-NULL. */
+ *   block_size      any positive size (the reference's is 16, kv_cache.h:27)
+ * Bits of *err_flag (when non-NULL; OR-ed in, never cleared):
+ *   bit 1  a block id outside [0, num_blocks), or a seq_len beyond the
+ *          table's capacity: clamped, never dereferenced out of the pool
+ *   bit 2  a sequence has more query tokens than max_query_len: its rows
+ *          beyond what the launch covers are not written */
 int iian_pa_attention(void *stream, const float *q, const void *k_pool, const void *v_pool,
                       int type_k, int type_v, int32_t num_blocks,
                       const int32_t *block_tables, int32_t max_blocks,
@@ -129,9 +142,14 @@ int iian_pa_attention(void *stream, const float *q, const void *k_pool, const vo
 
 /* Dequantises n_rows Q8_0 rows of row_elems values each (pool rows
  * rows_idx[i]) to f32, bit-exactly as ggml's dequantize_row_q8_0
- * (ggml-quants.c:553-567).  Exposes the values the attention kernels feed into
- * their arithmetic so that they can be checked bit for bit.  Rows outside
- * [0, n_cells) produce zeros. */
+ * (ggml-quants.c:553-567).  Rows outside [0, n_cells) produce zeros.
+ * These are the values the reference's dequantised path computes with.  The
+ * MFMA attention kernels enter K as exactly these values (int8 q in f16, the
+ * block scale d applied in fp32 after the product), but V as f16(q*d): q*d
+ * rounded once to f16, as P is.  A V value beyond the f16 range (|q*d| >
+ * 65504, possible only when a block scale exceeds 65504/127 ~ 516) becomes
+ * +-inf there, where the reference's fp32 value stays finite.  The general
+ * kernel enters both K and V as exactly these values. */
 int iian_pa_dequant_q8_0(void *stream, const void *pool, int64_t n_cells, const int64_t *rows_idx,
                          int64_t n_rows, int64_t row_elems, float *out);
 

@@ -48,6 +48,11 @@ class Case:
     softcap: float = 0.0
     causal: bool = True
     n_swa: int = 0
+    Dv: int = 0              # 0: same as D
+
+    def __post_init__(self):
+        if not self.Dv:
+            self.Dv = self.D
 
     @property
     def T(self):
@@ -57,13 +62,15 @@ class Case:
 def make_case(rng: np.random.Generator, H: int, Hkv: int, D: int, lens, nq, bs: int = 16, k_type: int = F16,
               v_type: Optional[int] = None, num_blocks: Optional[int] = None, shared_blocks: int = 0,
               shared_seqs: int = 0, softcap: float = 0.0, causal: bool = True, n_swa: int = 0,
-              pos_mode: str = "tail", quantize=None) -> Case:
+              pos_mode: str = "tail", quantize=None, Dv: Optional[int] = None) -> Case:
     """Random case: sequence s has lens[s] cells and its nq[s] query tokens sit
     at the last nq[s] positions (pos_mode 'tail') or at random positions
     ('random').  Blocks are a seeded random permutation of the pool; the first
     `shared_blocks` blocks of the first `shared_seqs` sequences are the same
-    physical blocks.  `quantize(rows f32) -> uint8 rows` is required for Q8_0."""
+    physical blocks.  `quantize(rows f32) -> uint8 rows` is required for Q8_0.
+    V rows hold Hkv*Dv elements (Dv defaults to D)."""
     v_type = k_type if v_type is None else v_type
+    Dv = D if Dv is None else Dv
     lens = np.asarray(lens, dtype=np.int64)
     nq = np.asarray(nq, dtype=np.int64)
     S = len(lens)
@@ -83,9 +90,8 @@ def make_case(rng: np.random.Generator, H: int, Hkv: int, D: int, lens, nq, bs: 
         bt[s, own:nblk[s]] = perm[cur:cur + nblk[s] - own]
         cur += int(nblk[s]) - own
     n_cells = num_blocks * bs
-    n_embd = Hkv * D
 
-    def pool(type_):
+    def pool(type_, n_embd):
         x = rng.standard_normal((n_cells, n_embd)).astype(np.float32)
         if type_ == F32:
             return x.view(np.uint8).reshape(n_cells, -1).copy()
@@ -93,7 +99,7 @@ def make_case(rng: np.random.Generator, H: int, Hkv: int, D: int, lens, nq, bs: 
             return x.astype(np.float16).view(np.uint8).reshape(n_cells, -1).copy()
         return quantize(x)
 
-    k_pool, v_pool = pool(k_type), pool(v_type)
+    k_pool, v_pool = pool(k_type, Hkv * D), pool(v_type, Hkv * Dv)
     seq_idx, pos = [], []
     for s in range(S):
         if pos_mode == "tail":
@@ -107,14 +113,15 @@ def make_case(rng: np.random.Generator, H: int, Hkv: int, D: int, lens, nq, bs: 
     T = len(pos)
     q = rng.standard_normal((T, H, D)).astype(np.float32)
     return Case(q, k_pool, v_pool, k_type, v_type, bt, lens.astype(np.int32), np.array(seq_idx, np.int32),
-                np.array(pos, np.int32), qsl, H, Hkv, D, bs, 1.0 / math.sqrt(D), softcap, causal, n_swa)
+                np.array(pos, np.int32), qsl, H, Hkv, D, bs, 1.0 / math.sqrt(D), softcap, causal, n_swa, Dv)
 
 
 def brute_force(c: Case, items=None) -> np.ndarray:
     """float64 softmax attention from the definition (paged_attn.cpp:121-144 semantics)."""
     T, H, D = c.q.shape
+    Dv = c.Dv
     gqa = H // c.Hkv
-    out = np.zeros((T, H, D), dtype=np.float64)
+    out = np.zeros((T, H, Dv), dtype=np.float64)
     cache = {}
     todo = range(T * H) if items is None else items
     for it in todo:
@@ -125,7 +132,7 @@ def brute_force(c: Case, items=None) -> np.ndarray:
             i = np.arange(L)
             cells = c.bt[s, i // c.bs].astype(np.int64) * c.bs + i % c.bs
             cache[s] = (decode_rows_f64(c.k_pool[cells], c.k_type, c.Hkv * D).reshape(L, c.Hkv, D),
-                        decode_rows_f64(c.v_pool[cells], c.v_type, c.Hkv * D).reshape(L, c.Hkv, D))
+                        decode_rows_f64(c.v_pool[cells], c.v_type, c.Hkv * Dv).reshape(L, c.Hkv, Dv))
         K, V = cache[s]
         hk = h // gqa
         p1 = int(c.pos[t])

@@ -41,16 +41,26 @@ def test_status_strings(lib):
 
 
 def test_supported_matrix(lib):
+    """iian_pa_supported accepts what paged_attn_supported accepts
+    (paged_attn.cpp:15-18: K and V each F16 or F32, in any pairing, no ALiBi;
+    any head size, Dv from the V pool, :163), widened to Q8_0, within the
+    documented remainder: head sizes must be multiples of 4 in [4, 512]
+    (multiples of 32 for a Q8_0 pool)."""
     from iian_amd import paged_attn_supported as sup
     F32, F16, Q8 = 0, 1, 8
-    assert sup(F16, F16, 0.0, 128)
-    assert sup(F16, F16, 0.0, 64) and sup(F16, F16, 0.0, 256)
-    assert sup(Q8, Q8, 0.0, 128) and sup(Q8, Q8, 0.0, 64) and sup(Q8, Q8, 0.0, 256)
-    assert not sup(F32, F32, 0.0, 128)          # F32 pools: KV write only
-    assert not sup(F16, F16, 8.0, 128)          # ALiBi (paged_attn.cpp:17)
-    assert not sup(F16, F32, 0.0, 128)          # mixed K/V types
-    assert not sup(F16, F16, 0.0, 96)           # head size without a kernel
-    assert not sup(F16, F16, 0.0, 128, 64)      # Dv != D
+    for tk in (F32, F16, Q8):
+        for tv in (F32, F16, Q8):
+            for d in (32, 64, 96, 128, 160, 256, 512):
+                assert sup(tk, tv, 0.0, d), (tk, tv, d)
+                assert sup(tk, tv, 0.0, d, 64) and sup(tk, tv, 0.0, 64, d)      # Dv != D
+            assert not sup(tk, tv, 8.0, 128)                                   # ALiBi (paged_attn.cpp:17)
+    for d in (4, 8, 80, 100, 112, 200, 508):
+        assert sup(F16, F16, 0.0, d) and sup(F32, F16, 0.0, d) and sup(F16, F32, 0.0, 64, d)
+        assert not sup(Q8, F16, 0.0, d) and not sup(F16, Q8, 0.0, 64, d)      # Q8_0 rows: 32-element blocks
+    # the remainder: not a multiple of 4, or above 512
+    for d in (0, 2, 6, 50, 130, 516, 576, 1024):
+        assert not sup(F16, F16, 0.0, d) and not sup(F32, F32, 0.0, 64, d)
+    assert not sup(2, F16, 0.0, 128) and not sup(F16, 2, 0.0, 128)           # Q4_0 pools are not KV types here
 
 
 def test_workspace_size(lib):
@@ -88,8 +98,10 @@ def call_attention(lib, **over):
     ({"q": None}, -1), ({"k": None}, -1), ({"bt": None}, -1), ({"out": None}, -1), ({"pos": None}, -1),
     ({"H": 6, "Hkv": 4}, -2), ({"Hkv": 0}, -2), ({"T": -1}, -2), ({"maxq": 5}, -2), ({"num_blocks": 0}, -2),
     ({"n_swa": -1}, -2), ({"softcap": -1.0}, -2), ({"scale": float("nan")}, -2), ({"q": 0x1004}, -2),
-    ({"tk": 8, "tv": 8, "D": 96, "Dv": 96}, -3), ({"tk": 0, "tv": 0}, -3), ({"tk": 1, "tv": 0}, -3), ({"D": 96, "Dv": 96}, -3),
-    ({"bs": 12}, -3), ({"bs": 4}, -3), ({"num_blocks": (1 << 28) + 1}, -3),   # more than 2^32 cells
+    ({"tk": 8, "tv": 8, "D": 80, "Dv": 80}, -3), ({"tk": 2, "tv": 2}, -3), ({"D": 130, "Dv": 130}, -3),
+    ({"D": 516, "Dv": 516}, -3), ({"Dv": 6}, -3), ({"bs": 0}, -2),
+    ({"num_blocks": (1 << 28) + 1}, -3),                      # more than 2^32 cells on the MFMA path
+    ({"tk": 0, "tv": 0, "max_blocks": 1 << 28}, -3),          # 2^32 cells in one sequence on the general path
     ({"ws": None}, -4), ({"ws_bytes": 16}, -4),
 ])
 def test_attention_rejects_invalid_arguments(lib, over, code):

@@ -19,7 +19,9 @@ import pytest
 
 from iian_amd import build as B
 
-KERNEL_SOURCES = ["pa_decode.hip", "pa_decode_q8.hip", "pa_prefill.hip", "pa_kv_write.hip"]
+# every device source of the library (pa_abi.hip is host code only)
+KERNEL_SOURCES = [s for s in B.SOURCES if s != "pa_abi.hip"]
+NO_MFMA = {"pa_kv_write.hip", "pa_general.hip", "pa_batch.hip", "pa_rope.hip"}
 PACKED_F32 = re.compile(r"^\s*v_pk_(add|mul|fma)_f32\b", re.M)
 NEG_MIX = re.compile(r"^\s*v_(fma|mad)_mix\w*\s[^\n]*,\s*-", re.M)
 
@@ -38,7 +40,7 @@ def test_no_packed_fp32_and_no_negated_mixed_fma(tmp_path):
     with ThreadPoolExecutor(len(KERNEL_SOURCES)) as ex:
         asms = dict(zip(KERNEL_SOURCES, ex.map(lambda s: device_asm(s, tmp_path), KERNEL_SOURCES)))
     for src, asm in asms.items():
-        assert "v_mfma" in asm or src == "pa_kv_write.hip", src   # the asm is the kernels'
+        assert "v_mfma" in asm or src in NO_MFMA, src   # the asm is the kernels'
         assert not PACKED_F32.search(asm), (src, PACKED_F32.search(asm).group(0))
         m = NEG_MIX.search(asm)
         assert m is None, (src, m.group(0) if m else None)

@@ -115,7 +115,7 @@ def test_dequant_q8_0_bit_exact(pa, oracle):
 
 def to_device(pa, c):
     k = pa.KVPool.wrap(torch.as_tensor(c.k_pool).cuda(), c.Hkv * c.D, c.k_type)
-    v = pa.KVPool.wrap(torch.as_tensor(c.v_pool).cuda(), c.Hkv * c.D, c.v_type)
+    v = pa.KVPool.wrap(torch.as_tensor(c.v_pool).cuda(), c.Hkv * c.Dv, c.v_type)
     nq = np.diff(c.qsl)
     batch = pa.PagedBatch(block_tables=torch.as_tensor(c.bt).cuda(), seq_lens=torch.as_tensor(c.seq_lens).cuda(),
                           query_start_loc=torch.as_tensor(c.qsl).cuda(), pos=torch.as_tensor(c.pos).cuda(),
@@ -124,8 +124,10 @@ def to_device(pa, c):
     return k, v, batch
 
 
-def gpu_attention(pa, c, err=None):
+def gpu_attention(pa, c, err=None, max_query_len=None):
     k, v, batch = to_device(pa, c)
+    if max_query_len is not None:
+        batch.max_query_len = max_query_len
     prm = pa.PagedAttnParams(scale=c.scale, softcap=c.softcap, causal=c.causal, n_swa=c.n_swa)
     out = pa.build_paged_attn(torch.as_tensor(c.q).cuda(), k, v, c.Hkv, prm, batch, err_flag=err)
     torch.cuda.synchronize()
@@ -134,7 +136,7 @@ def gpu_attention(pa, c, err=None):
 
 def oracle_attention(oracle, c, items=None):
     return oracle.paged_attention(c.q, c.k_pool, c.v_pool, c.k_type, c.v_type, c.bt, c.seq_lens, c.seq_idx, c.pos,
-                                  c.Hkv, c.D, c.bs, c.scale, softcap=c.softcap, causal=c.causal, n_swa=c.n_swa,
+                                  c.Hkv, c.Dv, c.bs, c.scale, softcap=c.softcap, causal=c.causal, n_swa=c.n_swa,
                                   n_threads=16, items=items)
 
 
@@ -231,14 +233,18 @@ def test_attention_growing_scores(pa, oracle, k_type, nq):
     assert e.max() <= TOL, e.max()
 
 
-def test_mixed_batch_on_a_side_stream_of_the_caller(pa, oracle):
-    """A prefill + decode batch forks its decode rows onto the library's side
-    stream and joins them back: issued on a non-default torch stream, three
-    back-to-back calls into three outputs are all complete once that stream
-    is synchronised."""
-    banner("mixed batch on a caller stream")
-    rng = np.random.default_rng(47)
-    c = make_case(rng, 32, 8, 128, [900, 1500, 700, 3000], [200, 1, 1, 1])
+@pytest.mark.parametrize("k_type,H,Hkv,D", [(Q8_0, 32, 8, 128), (F16, 16, 8, 256), (Q8_0, 16, 8, 256),
+                                           (F16, 32, 8, 128)])
+def test_mixed_batch_on_a_side_stream_of_the_caller(pa, oracle, k_type, H, Hkv, D):
+    """A prefill + decode batch over a Q8_0 pool or at head size 256 forks its
+    decode rows onto the library's side stream and joins them back (f16 at
+    head size 128 runs both in one launch): issued on a non-default torch
+    stream, three back-to-back calls into three outputs are all complete once
+    that stream is synchronised."""
+    banner(f"mixed batch on a caller stream k_type={k_type} D={D}")
+    rng = np.random.default_rng(47 + D + k_type)
+    c = make_case(rng, H, Hkv, D, [900, 1500, 700, 3000], [200, 1, 1, 1], k_type=k_type,
+                  quantize=oracle.quantize_q8_0)
     k, v, batch = to_device(pa, c)
     prm = pa.PagedAttnParams(scale=c.scale)
     qs = [rng.standard_normal(c.q.shape).astype(np.float32) for _ in range(3)]
@@ -283,9 +289,11 @@ def test_workspace_reuse_across_calls(pa, oracle):
         assert e.max() <= TOL, (it, e.max())
 
 
-# decode kernel (f16; Q8_0 spec-verify) and the mixed prefill launch, whose
-# decode workers merge split segments through tagged counters in the workspace
-SPLIT_CASES = [(F16, (1, 1, 1, 1)), (Q8_0, (5, 5, 5, 5)), (F16, (128, 1, 1, 1))]
+# decode kernel (f16; Q8_0 spec-verify), the mixed prefill launch, whose
+# decode workers merge split segments through tagged counters in the
+# workspace, and a Q8_0 mixed batch, whose decode rows run on the side stream
+# (a fork and join inside the captured graph)
+SPLIT_CASES = [(F16, (1, 1, 1, 1)), (Q8_0, (5, 5, 5, 5)), (F16, (128, 1, 1, 1)), (Q8_0, (128, 1, 1, 1))]
 
 
 @pytest.mark.parametrize("k_type,nqs", SPLIT_CASES)

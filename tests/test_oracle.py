@@ -22,7 +22,7 @@ def run_oracle(o, c, n_threads=4, items=None, **over):
     kw = dict(softcap=c.softcap, causal=c.causal, n_swa=c.n_swa)
     kw.update(over)
     return o.paged_attention(c.q, c.k_pool, c.v_pool, c.k_type, c.v_type, c.bt, c.seq_lens, c.seq_idx, c.pos,
-                             c.Hkv, c.D, c.bs, c.scale, n_threads=n_threads, items=items, **kw)
+                             c.Hkv, c.Dv, c.bs, c.scale, n_threads=n_threads, items=items, **kw)
 
 
 # ---------------------------------------------------------------- fp16
@@ -157,6 +157,15 @@ CASES = {
     "q8_0_kv": (8, 2, 128, [200, 64], [5, 1], {"k_type": Q8_0}),
     "prefix_shared": (8, 2, 64, [100, 120, 64], [4, 4, 1], {"shared_blocks": 4, "shared_seqs": 3}),
     "block_size_32": (4, 2, 64, [100, 31], [1, 2], {"bs": 32}),
+    # the combinations the reference accepts beyond f16/f16 at 64/128/256
+    # (paged_attn.cpp:15-18, 148-155; Dv from the V pool, :163)
+    "f32_k_f16_v": (4, 2, 64, [90, 33], [3, 1], {"k_type": F32, "v_type": F16}),
+    "phi3_d96": (8, 2, 96, [150, 40], [4, 1], {}),
+    "d80_f32": (4, 1, 80, [70], [2], {"k_type": F32}),
+    "dv_ne_d": (8, 2, 128, [120, 50], [2, 1], {"Dv": 64}),
+    "dv_gt_d_mixed": (4, 2, 64, [100], [3], {"Dv": 96, "k_type": F16, "v_type": F32}),
+    "block_size_12": (4, 2, 64, [100, 31], [1, 2], {"bs": 12}),
+    "q8_k_f16_v_d96": (8, 2, 96, [130], [2], {"k_type": Q8_0, "v_type": F16}),
 }
 
 
