@@ -16,6 +16,8 @@ ERR_ARG = -2
 ERR_UNSUPPORTED = -3
 ERR_WORKSPACE = -4
 ERR_HIP = -5
+ERR_SCRATCH = -6
+NOALLOC_SCRATCH_BYTES = 64 << 20
 
 TYPE_F32 = 0
 TYPE_F16 = 1
@@ -34,6 +36,9 @@ SIGNATURES = {
     "iian_pa_attention": (C.c_int, [_P, _P, _P, _P, C.c_int, C.c_int, _I32, _P, _I32, _P, _P, _P,
                                     _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32,
                                     C.c_float, C.c_float, _I32, _I32, _P, _P, C.c_size_t, _P]),
+    "iian_pa_attention_noalloc": (C.c_int, [_P, _P, _P, _P, C.c_int, C.c_int, _I32, _P, _I32, _P, _P, _P,
+                                            _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32,
+                                            C.c_float, C.c_float, _I32, _I32, _P, _P]),
     "iian_pa_dequant_q8_0": (C.c_int, [_P, _P, _I64, _P, _I64, _I64, _P]),
 }
 

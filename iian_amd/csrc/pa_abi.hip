@@ -93,6 +93,77 @@ WorkspaceLayout workspace_layout(int32_t n_seqs, int32_t n_head_kv, int32_t head
     return l;
 }
 
+// The bytes one call actually uses: records = workers + segments (a piece
+// (worker w, segment g) writes record w + g), each rec_stride floats, with
+// rec_heads * decode_rows (m, l) pairs; the segment table; a merge counter per
+// (sequence, kv head).  Never more than workspace_layout's upper bound.
+WorkspaceLayout exact_layout(const AttnParams &p) {
+    const size_t nseg = p.rec_heads > 1 ? (size_t) p.S : (size_t) p.S * p.Hkv;
+    const size_t records = (size_t) p.sk_workers + nseg;
+    WorkspaceLayout l;
+    l.o = 0;
+    l.ml = align256(records * (size_t) p.rec_stride * sizeof(float));
+    l.seg = l.ml + align256(records * p.rec_heads * p.decode_rows * 2 * sizeof(float));
+    l.ctr = l.seg + align256(nseg * sizeof(int2));
+    l.total = l.ctr + align256((size_t) p.S * p.Hkv * sizeof(uint64_t));
+    return l;
+}
+
+// ---- Scratch of the no-allocation entry point (iian_pa_attention_noalloc) ----
+//
+// A file-scope device array, one copy per GPU, living until the process
+// ends.  kScratchBytes covers every BASELINE configuration's call (the
+// largest, Q8_0 spec-verify at 128 sequences x 8 kv heads, uses 34 MB).  On
+// the host, `scratch` names a stand-in, not device memory: its device
+// address is taken once per device with hipGetSymbolAddress (with that
+// device current) and only that address is ever handed to kernels.
+constexpr size_t kScratchBytes = (size_t) 64 << 20;
+static __device__ __align__(256) char scratch[kScratchBytes];
+
+// Device address of `scratch` on device dev (nullptr when it cannot be taken).
+char *scratch_address(int dev) {
+    static std::atomic<char *> addr[kMaxDevices];
+    if (dev < 0 || dev >= kMaxDevices) return nullptr;
+    char *a = addr[dev].load(std::memory_order_acquire);
+    if (a) return a;
+    int cur = 0;
+    if (hipGetDevice(&cur) != hipSuccess) return nullptr;
+    if (cur != dev && hipSetDevice(dev) != hipSuccess) return nullptr;
+    void *ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (cur != dev && hipSetDevice(cur) != hipSuccess) return nullptr;
+    if (e != hipSuccess || !ptr) return nullptr;
+    addr[dev].store((char *) ptr, std::memory_order_release);
+    return (char *) ptr;
+}
+
+// Where a call's workspace comes from: the caller's buffer (iian_pa_attention;
+// at least iian_pa_workspace_size bytes, any alignment) or the library's
+// scratch on the stream's device (iian_pa_attention_noalloc).
+struct WsSource {
+    void *base;
+    size_t bytes;
+    bool scratch;
+};
+
+// 256-aligned base of `need` bytes of the call's workspace, or a status.
+int ws_resolve(const WsSource &src, hipStream_t st, size_t need, char **ws) {
+    if (!src.scratch) {
+        const char *b = (const char *) (((uintptr_t) src.base + 255) & ~(uintptr_t) 255);
+        if (need > src.bytes - (size_t) (b - (const char *) src.base)) return IIAN_PA_ERR_WORKSPACE;
+        *ws = (char *) b;
+        return IIAN_PA_OK;
+    }
+    if (need > kScratchBytes) return IIAN_PA_ERR_SCRATCH;
+    int dev = 0;
+    if (st != nullptr ? hipStreamGetDevice(st, &dev) != hipSuccess : hipGetDevice(&dev) != hipSuccess)
+        return IIAN_PA_ERR_HIP;
+    char *a = scratch_address(dev);
+    if (!a) return IIAN_PA_ERR_HIP;
+    *ws = a;
+    return IIAN_PA_OK;
+}
+
 // Tags of the mixed launch's merge counters: one per call, 48 bits, counting
 // up from a random start, so that workspace bytes the library never wrote
 // pass for a counter of the current call only with probability 2^-48 per
@@ -181,6 +252,7 @@ const char *iian_pa_status_string(int status) {
         case IIAN_PA_ERR_UNSUPPORTED: return "unsupported KV type, head size or ALiBi";
         case IIAN_PA_ERR_WORKSPACE: return "workspace missing or too small";
         case IIAN_PA_ERR_HIP: return "HIP runtime error";
+        case IIAN_PA_ERR_SCRATCH: return "the call needs more than the library's 64 MiB scratch (iian_pa_attention_noalloc)";
         default: return "unknown status";
     }
 }
@@ -234,14 +306,14 @@ size_t iian_pa_workspace_size(int32_t n_tokens, int32_t n_seqs, int32_t n_head, 
 
 namespace {
 
-// The attention call behind iian_pa_attention, on a workspace of ws_bytes
-// bytes at ws (any alignment; at least workspace_layout(...).total + 256).
+// The attention call behind iian_pa_attention and iian_pa_attention_noalloc,
+// on the workspace `src` names.
 int run_attention(hipStream_t st, const float *q, const void *k_pool, const void *v_pool, int type_k, int type_v,
                   int32_t num_blocks, const int32_t *block_tables, int32_t max_blocks, const int32_t *seq_lens,
                   const int32_t *query_start_loc, const int32_t *pos, int32_t n_tokens, int32_t n_seqs,
                   int32_t max_query_len, int32_t n_head, int32_t n_head_kv, int32_t head_dim, int32_t head_dim_v,
                   int32_t block_size, float scale, float softcap, int32_t causal, int32_t n_swa, float *out,
-                  void *workspace, size_t workspace_bytes, int32_t *err_flag) {
+                  const WsSource &src, int32_t *err_flag) {
     if (n_tokens < 0 || n_seqs < 0 || max_query_len < 0) return IIAN_PA_ERR_ARG;
     if (n_tokens == 0 || n_seqs == 0) return IIAN_PA_OK;
     if (!q || !k_pool || !v_pool || !block_tables || !seq_lens || !query_start_loc || !pos || !out)
@@ -254,8 +326,9 @@ int run_attention(hipStream_t st, const float *q, const void *k_pool, const void
     if (((uintptr_t) q | (uintptr_t) k_pool | (uintptr_t) v_pool | (uintptr_t) out) & 15) return IIAN_PA_ERR_ARG;
     const int cus = stream_device_cus(st);
     const WorkspaceLayout wl = workspace_layout(n_seqs, n_head_kv, head_dim_v, cus);
-    if (!workspace || workspace_bytes < wl.total + 256) return IIAN_PA_ERR_WORKSPACE;
-    char *ws = (char *) (((uintptr_t) workspace + 255) & ~(uintptr_t) 255);
+    // a caller's workspace must hold iian_pa_workspace_size bytes, whatever this call uses
+    if (!src.scratch && (!src.base || src.bytes < wl.total + 256)) return IIAN_PA_ERR_WORKSPACE;
+    char *ws = nullptr;
     int64_t kr, vr;
     if (row_bytes(type_k, (int64_t) n_head_kv * head_dim, kr) || row_bytes(type_v, (int64_t) n_head_kv * head_dim_v, vr))
         return IIAN_PA_ERR_ARG;
@@ -308,8 +381,12 @@ int run_attention(hipStream_t st, const float *q, const void *k_pool, const void
         const size_t per_split = (size_t) n_tokens * n_head * (size_t) (head_dim_v + 2) * sizeof(float) + 512;
         ns = std::min<int64_t>(ns, (int64_t) (wl.total / per_split));
         g.n_split = (int) std::max<int64_t>(ns, 1);
+        const size_t o_bytes = align256((size_t) n_tokens * n_head * g.n_split * head_dim_v * sizeof(float));
+        const size_t need = g.n_split > 1 ? o_bytes + (size_t) n_tokens * n_head * g.n_split * 2 * sizeof(float) : 0;
+        const int rc = ws_resolve(src, st, need, &ws);
+        if (rc) return rc;
         g.part_o = (float *) ws;
-        g.part_ml = (float *) (ws + align256((size_t) n_tokens * n_head * g.n_split * head_dim_v * sizeof(float)));
+        g.part_ml = (float *) (ws + o_bytes);
         return launch_general(g, type_k, type_v, st) == hipSuccess ? IIAN_PA_OK : IIAN_PA_ERR_HIP;
     }
 
@@ -359,27 +436,34 @@ int run_attention(hipStream_t st, const float *q, const void *k_pool, const void
         p.sk_workers = (head_dim == 256 ? kF16DecodeWavesPerCuD256 : kF16DecodeWavesPerCu) * cus;
     }
     p.rec_stride = (int64_t) p.rec_heads * p.decode_rows * head_dim_v + kRecordPad;
-    p.part_o = (float *) (ws + wl.o);
-    p.part_ml = (float *) (ws + wl.ml);
-    p.seg_info = (int2 *) (ws + wl.seg);
-    p.seg_ctr = (uint64_t *) (ws + wl.ctr);
-    p.epoch = next_epoch();
-    if (max_rows <= p.decode_rows)
-        return launch_decode(p, head_dim, type_k, st) == hipSuccess ? IIAN_PA_OK : IIAN_PA_ERR_HIP;
-
+    const bool decode_only = max_rows <= p.decode_rows;
     // Mixed batch over an f16 pool (head size 64 or 128): one launch holds the
     // prefill workgroups and, after them, the decode rows' stream-K workers,
     // which fill the CUs the MFMA-bound prefill leaves, and merge their split
     // segments themselves.
-    if (type_k == IIAN_PA_TYPE_F16 && head_dim <= 128) {
-        p.sk_workers = kF16MixedDecodeWavesPerCu * cus;
+    const bool mixed_one_launch = !decode_only && type_k == IIAN_PA_TYPE_F16 && head_dim <= 128;
+    if (mixed_one_launch) p.sk_workers = kF16MixedDecodeWavesPerCu * cus;
+    const WorkspaceLayout xl = exact_layout(p);
+    const int rc = ws_resolve(src, st, xl.total, &ws);
+    if (rc) return rc;
+    p.part_o = (float *) (ws + xl.o);
+    p.part_ml = (float *) (ws + xl.ml);
+    p.seg_info = (int2 *) (ws + xl.seg);
+    p.seg_ctr = (uint64_t *) (ws + xl.ctr);
+    p.epoch = next_epoch();
+    if (decode_only) return launch_decode(p, head_dim, type_k, st) == hipSuccess ? IIAN_PA_OK : IIAN_PA_ERR_HIP;
+    if (mixed_one_launch)
         return launch_mixed_f16(p, head_dim, max_rows, st) == hipSuccess ? IIAN_PA_OK : IIAN_PA_ERR_HIP;
-    }
 
     // Other mixed batches: the decode rows (HBM-bound) run on a side stream
     // forked from and joined back into the caller's stream, beside the
     // MFMA-bound prefill kernel, which fills the CUs first and leaves its tail
-    // to the decode waves.
+    // to the decode waves.  The no-allocation entry point creates no stream:
+    // it runs both kernels in order on the caller's stream.
+    if (src.scratch) {
+        if (launch_prefill(p, head_dim, type_k, max_rows, st) != hipSuccess) return IIAN_PA_ERR_HIP;
+        return launch_decode(p, head_dim, type_k, st) == hipSuccess ? IIAN_PA_OK : IIAN_PA_ERR_HIP;
+    }
     const SideStream *side = side_stream_for(st);
     if (!side) return IIAN_PA_ERR_HIP;
     if (hipEventRecord(side->fork, st) != hipSuccess || hipStreamWaitEvent(side->stream, side->fork, 0) != hipSuccess)
@@ -403,10 +487,24 @@ int iian_pa_attention(void *stream, const float *q, const void *k_pool, const vo
                       int32_t max_query_len, int32_t n_head, int32_t n_head_kv, int32_t head_dim, int32_t head_dim_v,
                       int32_t block_size, float scale, float softcap, int32_t causal, int32_t n_swa, float *out,
                       void *workspace, size_t workspace_bytes, int32_t *err_flag) {
+    const WsSource src = {workspace, workspace_bytes, false};
     return run_attention((hipStream_t) stream, q, k_pool, v_pool, type_k, type_v, num_blocks, block_tables,
                          max_blocks, seq_lens, query_start_loc, pos, n_tokens, n_seqs, max_query_len, n_head,
-                         n_head_kv, head_dim, head_dim_v, block_size, scale, softcap, causal, n_swa, out, workspace,
-                         workspace_bytes, err_flag);
+                         n_head_kv, head_dim, head_dim_v, block_size, scale, softcap, causal, n_swa, out, src,
+                         err_flag);
+}
+
+int iian_pa_attention_noalloc(void *stream, const float *q, const void *k_pool, const void *v_pool, int type_k,
+                              int type_v, int32_t num_blocks, const int32_t *block_tables, int32_t max_blocks,
+                              const int32_t *seq_lens, const int32_t *query_start_loc, const int32_t *pos,
+                              int32_t n_tokens, int32_t n_seqs, int32_t max_query_len, int32_t n_head,
+                              int32_t n_head_kv, int32_t head_dim, int32_t head_dim_v, int32_t block_size, float scale,
+                              float softcap, int32_t causal, int32_t n_swa, float *out, int32_t *err_flag) {
+    const WsSource src = {nullptr, kScratchBytes, true};
+    return run_attention((hipStream_t) stream, q, k_pool, v_pool, type_k, type_v, num_blocks, block_tables,
+                         max_blocks, seq_lens, query_start_loc, pos, n_tokens, n_seqs, max_query_len, n_head,
+                         n_head_kv, head_dim, head_dim_v, block_size, scale, softcap, causal, n_swa, out, src,
+                         err_flag);
 }
 
 int iian_pa_dequant_q8_0(void *stream, const void *pool, int64_t n_cells, const int64_t *rows_idx, int64_t n_rows,

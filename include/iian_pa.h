@@ -41,8 +41,13 @@ enum {
     IIAN_PA_ERR_ARG = -2,          /* inconsistent sizes / shapes */
     IIAN_PA_ERR_UNSUPPORTED = -3,  /* dtype / head size / ALiBi not supported */
     IIAN_PA_ERR_WORKSPACE = -4,    /* workspace missing or too small */
-    IIAN_PA_ERR_HIP = -5           /* a HIP runtime call failed */
+    IIAN_PA_ERR_HIP = -5,          /* a HIP runtime call failed */
+    IIAN_PA_ERR_SCRATCH = -6       /* iian_pa_attention_noalloc: the call needs more than
+                                      IIAN_PA_NOALLOC_SCRATCH_BYTES of scratch */
 };
+
+/* Size of the library's per-GPU scratch array used by iian_pa_attention_noalloc. */
+#define IIAN_PA_NOALLOC_SCRATCH_BYTES ((size_t) 64 << 20)
 
 enum { IIAN_PA_TYPE_F32 = 0, IIAN_PA_TYPE_F16 = 1, IIAN_PA_TYPE_Q8_0 = 8 };
 
@@ -139,6 +144,34 @@ int iian_pa_attention(void *stream, const float *q, const void *k_pool, const vo
                       float scale, float softcap, int32_t causal, int32_t n_swa,
                       float *out, void *workspace, size_t workspace_bytes,
                       int32_t *err_flag);
+
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory: code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc.  iian_pa_attention without the workspace arguments: the
+ * call's scratch (stream-K or split records, segment table, merge counters)
+ * lives in a file-scope device array of IIAN_PA_NOALLOC_SCRATCH_BYTES (64 MiB)
+ * that the library holds on every GPU it runs on until the process ends.  The
+ * call allocates nothing (no hipMalloc, hipFree, stream or event creation; a
+ * mixed batch that iian_pa_attention splits over a side stream runs its two
+ * kernels in order on `stream` here).  Its first call on a device looks up
+ * that device's copy of the array once.  A call needing more scratch than the
+ * array holds returns IIAN_PA_ERR_SCRATCH before any launch (every BASELINE
+ * configuration fits; the largest uses 34 MB).  Nothing in the array needs
+ * clearing between calls: every record is written before it is read within a
+ * call, and the merge counters carry a per-call tag.  All calls on one GPU
+ * share the array, so calls that overlap on one GPU (different streams, or
+ * threads) race: the caller must order them.  Results equal
+ * iian_pa_attention's for the same arguments.  Arguments, semantics and
+ * *err_flag bits as iian_pa_attention. */
+int iian_pa_attention_noalloc(void *stream, const float *q, const void *k_pool, const void *v_pool,
+                              int type_k, int type_v, int32_t num_blocks,
+                              const int32_t *block_tables, int32_t max_blocks,
+                              const int32_t *seq_lens, const int32_t *query_start_loc,
+                              const int32_t *pos, int32_t n_tokens, int32_t n_seqs,
+                              int32_t max_query_len, int32_t n_head, int32_t n_head_kv,
+                              int32_t head_dim, int32_t head_dim_v, int32_t block_size,
+                              float scale, float softcap, int32_t causal, int32_t n_swa,
+                              float *out, int32_t *err_flag);
 
 /* Dequantises n_rows Q8_0 rows of row_elems values each (pool rows
  * rows_idx[i]) to f32, bit-exactly as ggml's dequantize_row_q8_0

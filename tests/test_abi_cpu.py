@@ -35,7 +35,8 @@ def test_library_exports_every_declared_symbol(lib):
 
 def test_status_strings(lib):
     from iian_amd import _lib
-    for code in (_lib.OK, _lib.ERR_NULL, _lib.ERR_ARG, _lib.ERR_UNSUPPORTED, _lib.ERR_WORKSPACE, _lib.ERR_HIP):
+    for code in (_lib.OK, _lib.ERR_NULL, _lib.ERR_ARG, _lib.ERR_UNSUPPORTED, _lib.ERR_WORKSPACE, _lib.ERR_HIP,
+                 _lib.ERR_SCRATCH):
         assert _lib.status_string(code) not in ("", "unknown status")
     assert _lib.status_string(12345) == "unknown status"
 
@@ -184,3 +185,21 @@ def test_host_wrappers_validate_before_launch():
     with pytest.raises(ValueError):
         build_paged_attn(torch.zeros((1, 4, 128), dtype=torch.float32).transpose(0, 1), pool, pool, 2,
                          PagedAttnParams(), b)
+
+
+def test_noalloc_rejects_a_call_beyond_its_scratch(lib):
+    """iian_pa_attention_noalloc checks its need against the 64 MiB scratch on
+    the host and returns IIAN_PA_ERR_SCRATCH before any launch (pointers are
+    fake: nothing may reach the device)."""
+    from iian_amd import _lib
+    f = lib.iian_pa_attention_noalloc
+    # 40000 decode sequences x 8 kv heads: ~2.7 GB of stream-K records
+    st = f(None, 0x1000, 0x2000, 0x3000, 1, 1, 1 << 20, 0x4000, 4, 0x5000, 0x6000, 0x7000, 40000, 40000, 1, 32, 8,
+           128, 128, 16, 0.1, 0.0, 1, 0, 0x8000, None)
+    assert st == _lib.ERR_SCRATCH
+    assert "64 MiB" in _lib.status_string(st)
+    # argument checks come first, as in iian_pa_attention
+    assert f(None, None, 0x2000, 0x3000, 1, 1, 64, 0x4000, 4, 0x5000, 0x6000, 0x7000, 4, 2, 2, 8, 2, 128, 128, 16,
+             0.1, 0.0, 1, 0, 0x8000, None) == _lib.ERR_NULL
+    assert f(None, 0x1000, 0x2000, 0x3000, 1, 1, 64, 0x4000, 4, 0x5000, 0x6000, 0x7000, 4, 2, 2, 8, 2, 130, 130, 16,
+             0.1, 0.0, 1, 0, 0x8000, None) == _lib.ERR_UNSUPPORTED
