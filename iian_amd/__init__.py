@@ -12,6 +12,8 @@ from .paged_attn import (  # noqa: F401
     KVPool,
     PagedAttnParams,
     PagedBatch,
+    RequestBlocks,
+    build_batch,
     build_paged_attn,
     dequant_q8_0,
     new_workspace,

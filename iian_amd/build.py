@@ -11,6 +11,7 @@ import os
 import shutil
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
@@ -18,7 +19,7 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libiian_pa.so"
 SOURCES = ["pa_abi.hip", "pa_decode.hip", "pa_decode_q8.hip", "pa_prefill.hip", "pa_prefill16.hip", "pa_general.hip",
-           "pa_kv_write.hip"]
+           "pa_kv_write.hip", "pa_batch.hip"]
 ARCH = "gfx950"
 
 # Packed-FP32 VALU ops are disabled for all device code: some of their forms
@@ -37,21 +38,25 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found: the ROCm toolchain is required to build libiian_pa.so")
 
 
+def _compile(cc: str, src: str, objdir: Path, verbose: bool) -> str:
+    obj = objdir / (Path(src).stem + ".o")
+    cmd = [cc, *HIPCC_FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {src}:\n{res.stderr}")
+    return str(obj)
+
+
 def build(verbose: bool = False) -> Path:
-    """Compile every HIP source for gfx950 and link libiian_pa.so; returns its path."""
+    """Compile every HIP source for gfx950 (in parallel) and link libiian_pa.so; returns its path."""
     cc = hipcc()
     objdir = PKG / "_build"
     objdir.mkdir(exist_ok=True)
-    objs = []
-    for src in SOURCES:
-        obj = objdir / (Path(src).stem + ".o")
-        cmd = [cc, *HIPCC_FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
-        if verbose:
-            print(" ".join(cmd), flush=True)
-        res = subprocess.run(cmd, capture_output=True, text=True)
-        if res.returncode != 0:
-            raise RuntimeError(f"hipcc failed on {src}:\n{res.stderr}")
-        objs.append(str(obj))
+    jobs = max(1, min(len(SOURCES), os.cpu_count() or 1, 8))
+    with ThreadPoolExecutor(jobs) as ex:
+        objs = list(ex.map(lambda src: _compile(cc, src, objdir, verbose), SOURCES))
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *objs]
     res = subprocess.run(cmd, capture_output=True, text=True)

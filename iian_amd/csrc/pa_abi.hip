@@ -507,6 +507,35 @@ int iian_pa_attention_noalloc(void *stream, const float *q, const void *k_pool, 
                          err_flag);
 }
 
+int iian_pa_build_batch(void *stream, const int32_t *block_ids, const int32_t *block_off,
+                        const int32_t *num_computed, const int32_t *n_new, int32_t n_seqs, int32_t n_tokens,
+                        int32_t block_size, int32_t max_blocks, int32_t num_blocks, int32_t *block_tables,
+                        int32_t *seq_lens, int32_t *query_start_loc, int32_t *pos, int64_t *slots,
+                        int32_t *err_flag) {
+    if (n_seqs < 0 || n_tokens < 0 || block_size <= 0 || max_blocks <= 0 || num_blocks <= 0) return IIAN_PA_ERR_ARG;
+    if (n_seqs == 0) return IIAN_PA_OK;
+    if (!block_off || !num_computed || !n_new || !block_tables || !seq_lens || !query_start_loc ||
+        (n_tokens > 0 && (!pos || !slots)))
+        return IIAN_PA_ERR_NULL;
+    BatchParams p = {};
+    p.block_ids = block_ids;
+    p.block_off = block_off;
+    p.num_computed = num_computed;
+    p.n_new = n_new;
+    p.block_tables = block_tables;
+    p.seq_lens = seq_lens;
+    p.qsl = query_start_loc;
+    p.pos = pos;
+    p.slots = slots;
+    p.err = err_flag;
+    p.S = n_seqs;
+    p.T = n_tokens;
+    p.block_size = block_size;
+    p.max_blocks = max_blocks;
+    p.num_blocks = num_blocks;
+    return launch_build_batch(p, (hipStream_t) stream) == hipSuccess ? IIAN_PA_OK : IIAN_PA_ERR_HIP;
+}
+
 int iian_pa_dequant_q8_0(void *stream, const void *pool, int64_t n_cells, const int64_t *rows_idx, int64_t n_rows,
                          int64_t row_elems, float *out) {
     if (n_rows < 0 || row_elems <= 0 || row_elems % 32 || n_cells < 0) return IIAN_PA_ERR_ARG;

@@ -44,6 +44,22 @@ hipError_t launch_mixed_f16(const AttnParams &p, int head_dim, int max_rows, hip
 // The 16-row-tile prefill kernel (pa_prefill16.hip), used at head size 256.
 hipError_t launch_prefill16(const AttnParams &p, int head_dim, int kv_type, int max_rows, hipStream_t stream);
 
+// Inputs and outputs of the batch-metadata kernel (pa_batch.hip).
+struct BatchParams {
+    const int32_t *block_ids;     // packed per-request block ids
+    const int32_t *block_off;     // [S+1] request s owns block_ids[block_off[s] .. block_off[s+1])
+    const int32_t *num_computed;  // [S]
+    const int32_t *n_new;         // [S]
+    int32_t *block_tables;        // [S][max_blocks]
+    int32_t *seq_lens;            // [S]
+    int32_t *qsl;                 // [S+1]
+    int32_t *pos;                 // [T]
+    int64_t *slots;               // [T]
+    int32_t *err;                 // nullable
+    int32_t S, T, block_size, max_blocks, num_blocks;
+};
+hipError_t launch_build_batch(const BatchParams &p, hipStream_t stream);
+
 // General fp32 path (pa_general.hip): any K/V types of F32, F16, Q8_0; head
 // sizes 4..512 in steps of 4; any block size.
 hipError_t launch_general(const GenParams &p, int type_k, int type_v, hipStream_t stream);

@@ -159,6 +159,71 @@ class PagedBatch:
                    max_query_len=int(counts.max()) if S else 0, block_size=block_size)
 
 
+@dataclass
+class RequestBlocks:
+    """Device copies of the per-request state iian_pa_build_batch reads: the
+    packed block ids of every scheduled request (KVRequestState::block_ids,
+    include/iian/kv_cache.h:93-97), the offsets of each request's ids, and its
+    computed-token and new-token counts (Request::num_computed_tokens,
+    ScheduledRequest::n_new_tokens)."""
+    block_ids: torch.Tensor      # int32 [sum of blocks]
+    block_off: torch.Tensor      # int32 [S+1]
+    num_computed: torch.Tensor   # int32 [S]
+    n_new: torch.Tensor          # int32 [S]
+
+    @classmethod
+    def pack(cls, block_ids: Sequence[Sequence[int]], num_computed: Sequence[int], n_new: Sequence[int],
+             device="cuda") -> "RequestBlocks":
+        S = len(block_ids)
+        if len(num_computed) != S or len(n_new) != S:
+            raise ValueError("one block list, computed count and new count per request")
+        off = np.zeros(S + 1, dtype=np.int64)
+        off[1:] = np.cumsum([len(b) for b in block_ids])
+        if off[-1] > np.iinfo(np.int32).max:
+            raise ValueError("too many blocks")
+        flat = np.concatenate([np.asarray(b, dtype=np.int32) for b in block_ids]) if off[-1] else np.zeros(1, np.int32)
+        t = lambda a: torch.as_tensor(np.ascontiguousarray(a, dtype=np.int32), device=device)
+        return cls(block_ids=t(flat), block_off=t(off), num_computed=t(num_computed), n_new=t(n_new))
+
+
+def build_batch(req: RequestBlocks, n_tokens: int, block_size: int, max_blocks: int, num_blocks: int,
+                max_query_len: Optional[int] = None, out: Optional[PagedBatch] = None,
+                err_flag: Optional[torch.Tensor] = None) -> PagedBatch:
+    """The step's PagedBatch built on the device by iian_pa_build_batch from
+    the requests' block ids and counts (the work of Engine::step's UBatch
+    loop, src/iian/engine.cpp:491-535, without expanding cells on the host).
+    `out` (optional) supplies the output tensors, which makes the call
+    allocation-free."""
+    S = int(req.n_new.shape[0])
+    dev = req.n_new.device
+    for name in ("block_ids", "block_off", "num_computed", "n_new"):
+        t = getattr(req, name)
+        if t.dtype != torch.int32 or t.dim() != 1 or not t.is_contiguous() or t.device != dev:
+            raise ValueError(f"req.{name} must be a contiguous int32 1-d tensor on {dev}")
+    if req.block_off.shape[0] != S + 1 or req.num_computed.shape[0] != S:
+        raise ValueError("block_off must have S+1 entries and num_computed S")
+    if out is None:
+        out = PagedBatch(block_tables=torch.empty((S, max_blocks), dtype=torch.int32, device=dev),
+                         seq_lens=torch.empty(S, dtype=torch.int32, device=dev),
+                         query_start_loc=torch.empty(S + 1, dtype=torch.int32, device=dev),
+                         pos=torch.empty(n_tokens, dtype=torch.int32, device=dev),
+                         slots=torch.empty(n_tokens, dtype=torch.int64, device=dev),
+                         max_query_len=0, block_size=block_size)
+    else:
+        if tuple(out.block_tables.shape) != (S, max_blocks) or out.pos.shape[0] != n_tokens:
+            raise ValueError("out does not match the batch shape")
+        _check_batch(out, dev)
+    out.max_query_len = int(max_query_len) if max_query_len is not None else out.max_query_len
+    out.block_size = block_size
+    st = _lib.load().iian_pa_build_batch(_stream(), req.block_ids.data_ptr(), req.block_off.data_ptr(),
+                                         req.num_computed.data_ptr(), req.n_new.data_ptr(), S, n_tokens, block_size,
+                                         max_blocks, num_blocks, out.block_tables.data_ptr(), out.seq_lens.data_ptr(),
+                                         out.query_start_loc.data_ptr(), out.pos.data_ptr(), out.slots.data_ptr(),
+                                         _ptr(err_flag))
+    _lib.check("iian_pa_build_batch", st)
+    return out
+
+
 def paged_attn_supported(type_k: int, type_v: int, max_alibi_bias: float, head_dim: int = 128,
                          head_dim_v: Optional[int] = None) -> bool:
     """src/iian/paged_attn.cpp:15-18, as supported by the gfx950 kernels."""

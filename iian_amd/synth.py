@@ -146,6 +146,20 @@ def _tables(sp: Spec, rng: np.random.Generator) -> np.ndarray:
     return bt
 
 
+def request_blocks(sp: Spec):
+    """The per-request state behind the workload's batch, as the scheduler
+    holds it: each request's block ids (its block-table row, the blocks its
+    context uses), its computed-token count (context before this step) and
+    its new-token count.  Same seeded tables as build()."""
+    rng = np.random.default_rng(sp.seed + 1000)
+    bt = _tables(sp, rng)
+    bs = sp.block_size
+    nblk = (sp.seq_lens + bs - 1) // bs
+    ids = [bt[s, :nblk[s]].copy() for s in range(len(sp.seq_lens))]
+    n_new = sp.n_q.astype(np.int32)
+    return ids, (sp.seq_lens - sp.n_q).astype(np.int32), n_new
+
+
 def _fill_randn(dst: torch.Tensor, gen: torch.Generator, chunk: int = 1 << 26) -> None:
     """dst (f16 view, any shape) <- N(0,1) values cast to f16, in chunks."""
     flat = dst.view(-1)

@@ -173,6 +173,36 @@ int iian_pa_attention_noalloc(void *stream, const float *q, const void *k_pool, 
                               float scale, float softcap, int32_t causal, int32_t n_swa,
                               float *out, int32_t *err_flag);
 
+/* Builds the arrays iian_pa_attention and iian_pa_kv_write read for one
+ * engine step on the device, from the per-request state the scheduler holds,
+ * in place of the host loop of Engine::step that expands every request's
+ * block table into absolute cells (src/iian/engine.cpp:491-535, cell_of of
+ * include/iian/kv_cache.h:135-137): the host uploads sum(blocks) + 3*S
+ * integers instead of sum(context) cells.  For request s (batch order):
+ *   block_ids[block_off[s] .. block_off[s+1])   KVRequestState::block_ids
+ *                                                (kv_cache.h:93-97)
+ *   num_computed[s]                              Request::num_computed_tokens
+ *   n_new[s]                                     ScheduledRequest::n_new_tokens
+ * it writes
+ *   seq_lens[s] = num_computed[s] + n_new[s]
+ *   query_start_loc[s] = n_new[0] + ... + n_new[s-1], query_start_loc[S] = n_tokens
+ *   block_tables[s][b] = the request's b-th block id for the blocks its
+ *                        context uses, 0 after them (int32 [S][max_blocks])
+ *   pos[t] = num_computed[s] + i and
+ *   slots[t] = block_ids[pos/bs]*bs + pos%bs     for its i-th new token t
+ *                                                (engine.cpp:508-513)
+ * All arrays are device memory.  Bits of *err_flag (when non-NULL):
+ *   bit 0  a new token has no block (its slot is -1, which the KV write skips)
+ *   bit 1  a block id outside [0, num_blocks)
+ *   bit 3  counts inconsistent: negative counts, a request whose blocks do
+ *          not cover its context or exceed max_blocks, or new tokens that
+ *          do not sum to n_tokens */
+int iian_pa_build_batch(void *stream, const int32_t *block_ids, const int32_t *block_off,
+                        const int32_t *num_computed, const int32_t *n_new, int32_t n_seqs, int32_t n_tokens,
+                        int32_t block_size, int32_t max_blocks, int32_t num_blocks, int32_t *block_tables,
+                        int32_t *seq_lens, int32_t *query_start_loc, int32_t *pos, int64_t *slots,
+                        int32_t *err_flag);
+
 /* Dequantises n_rows Q8_0 rows of row_elems values each (pool rows
  * rows_idx[i]) to f32, bit-exactly as ggml's dequantize_row_q8_0
  * (ggml-quants.c:553-567).  Rows outside [0, n_cells) produce zeros.

@@ -47,6 +47,8 @@ def lib() -> C.CDLL:
             getattr(L, n).argtypes = [P, P, I64]
         L.pao_set_rows.restype = C.c_int
         L.pao_set_rows.argtypes = [P, I64, I64, P, P, I64, C.c_int]
+        L.pao_build_batch.restype = C.c_int64
+        L.pao_build_batch.argtypes = [P, P, P, P, I32, I32, I32, P, P, P, P, P, P, P]
         L.pao_paged_attention.restype = C.c_int
         L.pao_paged_attention.argtypes = [P, P, P, C.c_int, C.c_int, P, I32, P, P, P, I32, I32, I32, I32, I32,
                                           I32, I32, C.c_float, C.c_float, I32, I32, P, I32, P, I64]
@@ -145,3 +147,31 @@ def paged_attention(q: np.ndarray, k_pool: np.ndarray, v_pool: np.ndarray, k_typ
     if st != 0:
         raise ValueError(f"pao_paged_attention rejected its arguments ({st})")
     return out
+
+
+def build_batch(block_ids, num_computed, n_new, block_size: int, max_blocks: int) -> dict:
+    """Engine::step's UBatch arrays (engine.cpp:491-535) restated (pa_oracle.c
+    pao_build_batch): block tables, seq_lens, query_start_loc, pos, slots, plus
+    seq_idx and the expanded per-request cell lists."""
+    S = len(block_ids)
+    off = np.zeros(S + 1, dtype=np.int32)
+    off[1:] = np.cumsum([len(b) for b in block_ids])
+    flat = np.ascontiguousarray(np.concatenate([np.asarray(b, np.int32) for b in block_ids]) if off[-1]
+                                else np.zeros(1, np.int32), dtype=np.int32)
+    nc = np.ascontiguousarray(num_computed, dtype=np.int32)
+    nn = np.ascontiguousarray(n_new, dtype=np.int32)
+    T = int(nn.sum())
+    L = nc.astype(np.int64) + nn
+    bt = np.empty((S, max_blocks), np.int32)
+    sl = np.empty(S, np.int32)
+    qsl = np.empty(S + 1, np.int32)
+    pos = np.empty(max(T, 1), np.int32)
+    slots = np.empty(max(T, 1), np.int64)
+    seq_idx = np.empty(max(T, 1), np.int32)
+    cells = np.empty(max(int(L.sum()), 1), np.int64)
+    got = lib().pao_build_batch(_p(flat), _p(off), _p(nc), _p(nn), S, block_size, max_blocks, _p(bt), _p(sl),
+                                _p(qsl), _p(pos), _p(slots), _p(seq_idx), _p(cells))
+    if got < 0:
+        raise ValueError("pao_build_batch rejected its arguments")
+    return dict(block_tables=bt, seq_lens=sl, query_start_loc=qsl, pos=pos[:T], slots=slots[:T],
+                seq_idx=seq_idx[:T], cells=np.split(cells[:int(L.sum())], np.cumsum(L)[:-1]))

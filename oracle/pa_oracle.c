@@ -338,3 +338,48 @@ int pao_paged_attention(const float *q, const void *k_pool, const void *v_pool,
     for (int i = 0; i < nth; i++) pthread_join(tid[i], NULL);
     return 0;
 }
+
+/* ---------------------------------------------------------- batch build */
+
+/* The arrays of one engine step that the paged op reads, built the way
+ * Engine::step builds its UBatch (src/iian/engine.cpp:491-535) from the
+ * scheduler's per-request state, then compressed to block tables:
+ *   for request s (batch order), with n_ctx = num_computed[s] + n_new[s]:
+ *     cells[i] = cell_of(kv, i), i < n_ctx          (engine.cpp:501-507;
+ *                = block_ids[i/bs]*bs + i%bs          kv_cache.h:135-137)
+ *     for i in [num_computed, n_ctx): pos = i, seq_idx = s, slot = cell_of(i)
+ *                                                    (engine.cpp:508-513)
+ *   block_tables[s][b] = block_ids[b] for b < ceil(n_ctx/bs), 0 after;
+ *   seq_lens[s] = n_ctx; qsl = exclusive prefix sum of n_new.
+ * Request s's block ids are block_ids[block_off[s] .. block_off[s+1]).
+ * `cells` (nullable) receives every request's expanded cell list, one after
+ * the other; `seq_idx` (nullable) the per-token request index.  Returns the
+ * token count T, or -1 when a request's blocks do not cover its context or
+ * outnumber max_blocks (the engine's allocate_slots guarantees both,
+ * include/iian/kv_cache.h:125-127). */
+int64_t pao_build_batch(const int32_t *block_ids, const int32_t *block_off, const int32_t *num_computed,
+                        const int32_t *n_new, int32_t S, int32_t block_size, int32_t max_blocks,
+                        int32_t *block_tables, int32_t *seq_lens, int32_t *qsl, int32_t *pos, int64_t *slots,
+                        int32_t *seq_idx, int64_t *cells) {
+    int64_t T = 0, nc = 0;
+    qsl[0] = 0;
+    for (int32_t s = 0; s < S; s++) {
+        const int32_t *ids = block_ids + block_off[s];
+        const int32_t nb = block_off[s + 1] - block_off[s];
+        const int32_t n_ctx = num_computed[s] + n_new[s];
+        if ((int64_t) nb * block_size < n_ctx || nb > max_blocks) return -1;
+        for (int32_t i = 0; i < n_ctx && cells; i++)
+            cells[nc++] = (int64_t) ids[i / block_size] * block_size + i % block_size;
+        for (int32_t i = num_computed[s]; i < n_ctx; i++) {
+            pos[T] = i;
+            if (seq_idx) seq_idx[T] = s;
+            slots[T] = (int64_t) ids[i / block_size] * block_size + i % block_size;
+            T++;
+        }
+        const int32_t used = (n_ctx + block_size - 1) / block_size;
+        for (int32_t b = 0; b < max_blocks; b++) block_tables[(int64_t) s * max_blocks + b] = b < used ? ids[b] : 0;
+        seq_lens[s] = n_ctx;
+        qsl[s + 1] = (int32_t) T;
+    }
+    return T;
+}

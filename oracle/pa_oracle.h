@@ -86,6 +86,18 @@ int pao_paged_attention(const float *q, const void *k_pool, const void *v_pool,
                         float *out, int32_t n_threads,
                         const int64_t *items, int64_t n_items);
 
+/* The arrays of one engine step the paged op reads (block tables, seq_lens,
+ * query_start_loc, pos, slots), built as Engine::step builds its UBatch
+ * (src/iian/engine.cpp:491-535) from per-request block ids, computed-token
+ * counts and new-token counts, then compressed to block tables (padded with
+ * 0).  `seq_idx` and `cells` (the expanded per-request cell lists) are
+ * optional outputs.  Returns the token count, or -1 when a request's blocks do
+ * not cover its context or exceed max_blocks. */
+int64_t pao_build_batch(const int32_t *block_ids, const int32_t *block_off, const int32_t *num_computed,
+                        const int32_t *n_new, int32_t S, int32_t block_size, int32_t max_blocks,
+                        int32_t *block_tables, int32_t *seq_lens, int32_t *qsl, int32_t *pos, int64_t *slots,
+                        int32_t *seq_idx, int64_t *cells);
+
 #ifdef __cplusplus
 }
 #endif

@@ -292,3 +292,43 @@ def test_invalid_arguments_rejected(oracle):
     with pytest.raises(ValueError):
         oracle.paged_attention(c.q, c.k_pool, c.v_pool, F16, F16, c.bt, c.seq_lens, np.array([3], np.int32),
                                c.pos, c.Hkv, c.D, c.bs, c.scale)
+
+
+# ---------------------------------------------------------------- batch build
+
+@pytest.mark.parametrize("name", ["cfg2", "cfg3", "cfg4", "cfg3_p0"])
+def test_build_batch_restates_the_engine_ubatch(oracle, name):
+    """pao_build_batch against the closed forms of engine.cpp:501-513
+    (cells[i] = ids[i/bs]*bs + i%bs for every context token; the new tokens
+    are the last n_new positions, slot = cells[pos]) and against
+    PagedBatch.from_ubatch run on that UBatch (the compression the GPU path
+    takes as its input format)."""
+    from iian_amd import PagedBatch, synth
+    sp = synth.spec(name)
+    ids, nc, nn = synth.request_blocks(sp)
+    bs = sp.block_size
+    max_blocks = max(len(b) for b in ids)
+    o = oracle.build_batch(ids, nc, nn, bs, max_blocks)
+    L = nc.astype(np.int64) + nn
+    pos, seq_idx, slots = [], [], []
+    for s, b in enumerate(ids):
+        i = np.arange(L[s])
+        cells = np.asarray(b, np.int64)[i // bs] * bs + i % bs
+        assert np.array_equal(o["cells"][s], cells)
+        pos += list(range(nc[s], L[s]))
+        seq_idx += [s] * int(nn[s])
+        slots += list(cells[nc[s]:])
+    assert np.array_equal(o["pos"], pos) and np.array_equal(o["seq_idx"], seq_idx)
+    assert np.array_equal(o["slots"], slots)
+    host = PagedBatch.from_ubatch(o["pos"], o["seq_idx"], o["slots"], o["cells"], block_size=bs, device="cpu")
+    assert np.array_equal(host.block_tables.numpy(), o["block_tables"])
+    assert np.array_equal(host.seq_lens.numpy(), o["seq_lens"])
+    assert np.array_equal(host.query_start_loc.numpy(), o["query_start_loc"])
+    assert host.max_query_len == int(nn.max())
+
+
+def test_build_batch_rejects_short_block_lists(oracle):
+    with pytest.raises(ValueError):
+        oracle.build_batch([[3, 4], [5]], [20, 0], [20, 1], 16, 4)   # 40 tokens in 2 blocks of 16
+    with pytest.raises(ValueError):
+        oracle.build_batch([[3, 4, 5]], [0], [40], 16, 2)            # more blocks than the table row holds
