@@ -13,11 +13,13 @@ from .paged_attn import (  # noqa: F401
     PagedAttnParams,
     PagedBatch,
     RequestBlocks,
+    RopeParams,
     build_batch,
     build_paged_attn,
     dequant_q8_0,
     new_workspace,
     paged_attn_supported,
+    rope_set_rows_kv,
     row_bytes,
     set_rows,
     set_rows_kv,

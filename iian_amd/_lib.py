@@ -40,8 +40,18 @@ SIGNATURES = {
                                             _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32,
                                             C.c_float, C.c_float, _I32, _I32, _P, _P]),
     "iian_pa_build_batch": (C.c_int, [_P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P]),
+    "iian_pa_rope_kv_write": (C.c_int, [_P, _P, _P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _I32, _P, _P, _P, _I64,
+                                        C.c_int, C.c_int, _P]),
     "iian_pa_dequant_q8_0": (C.c_int, [_P, _P, _I64, _P, _I64, _I64, _P]),
 }
+
+
+class RopeParams(C.Structure):
+    """iian_pa_rope_params of include/iian_pa.h."""
+    _fields_ = [("n_dims", C.c_int32), ("mode", C.c_int32), ("n_ctx_orig", C.c_int32),
+                ("freq_base", C.c_float), ("freq_scale", C.c_float), ("ext_factor", C.c_float),
+                ("attn_factor", C.c_float), ("beta_fast", C.c_float), ("beta_slow", C.c_float),
+                ("freq_factors", C.c_void_p)]
 
 _lib = None
 

@@ -536,6 +536,66 @@ int iian_pa_build_batch(void *stream, const int32_t *block_ids, const int32_t *b
     return launch_build_batch(p, (hipStream_t) stream) == hipSuccess ? IIAN_PA_OK : IIAN_PA_ERR_HIP;
 }
 
+int iian_pa_rope_kv_write(void *stream, const float *k_rows, const float *v_rows, const float *q_in, float *q_out,
+                          const int32_t *pos, const int64_t *slots, int64_t n_rows, int32_t n_head, int32_t n_head_kv,
+                          int32_t head_dim, int32_t head_dim_v, const iian_pa_rope_params *rope, void *k_pool,
+                          void *v_pool, int64_t n_cells, int type_k, int type_v, int32_t *err_flag) {
+#pragma clang fp contract(off)
+    if (n_rows < 0 || n_cells < 0 || n_head < 0 || n_head_kv <= 0 || head_dim <= 0 || head_dim_v <= 0)
+        return IIAN_PA_ERR_ARG;
+    if (n_rows == 0) return IIAN_PA_OK;
+    if (!k_rows || !v_rows || !pos || !slots || !rope || !k_pool || !v_pool) return IIAN_PA_ERR_NULL;
+    if ((q_in == nullptr) != (q_out == nullptr) || (q_in && n_head <= 0)) return IIAN_PA_ERR_ARG;
+    if (n_rows > INT32_MAX) return IIAN_PA_ERR_ARG;
+    if (rope->mode != 0 && rope->mode != 2) return IIAN_PA_ERR_UNSUPPORTED;
+    if (rope->n_dims <= 0 || rope->n_dims % 2 || rope->n_dims > head_dim || head_dim % 2 || head_dim_v % 2 ||
+        !(rope->freq_base > 0.0f) || !(rope->freq_scale > 0.0f))
+        return IIAN_PA_ERR_ARG;
+    int64_t kb, vb;
+    int rc = row_bytes(type_k, (int64_t) n_head_kv * head_dim, kb);
+    if (rc) return rc;
+    rc = row_bytes(type_v, (int64_t) n_head_kv * head_dim_v, vb);
+    if (rc) return rc;
+    if ((int64_t) n_head_kv * head_dim > 16384 || (int64_t) n_head_kv * head_dim_v > INT32_MAX / 2 ||
+        (int64_t) n_head * head_dim > INT32_MAX / 2)
+        return IIAN_PA_ERR_ARG;
+    RopeParams p = {};
+    p.k_rows = k_rows;
+    p.v_rows = v_rows;
+    p.q_in = q_in;
+    p.q_out = q_out;
+    p.pos = pos;
+    p.slots = slots;
+    p.k_pool = k_pool;
+    p.v_pool = v_pool;
+    p.freq_factors = rope->freq_factors;
+    p.err = err_flag;
+    p.n_cells = n_cells;
+    p.T = (int32_t) n_rows;
+    p.H = n_head;
+    p.Hkv = n_head_kv;
+    p.D = head_dim;
+    p.Dv = head_dim_v;
+    p.n_dims = rope->n_dims;
+    p.mode = rope->mode;
+    // the per-call constants of ggml's CPU rope, computed as it computes them
+    // on its host (ggml-cpu/ops.cpp:6144-6146, 5969; ggml.c:4418-4430)
+    p.theta_scale = powf(rope->freq_base, -2.0f / rope->n_dims);
+    const int n_dims = rope->n_dims;
+    const float start = floorf(n_dims * logf(rope->n_ctx_orig / (rope->beta_fast * 2 * (float) M_PI)) /
+                               (2 * logf(rope->freq_base)));
+    const float end = ceilf(n_dims * logf(rope->n_ctx_orig / (rope->beta_slow * 2 * (float) M_PI)) /
+                            (2 * logf(rope->freq_base)));
+    p.corr0 = std::max(0.0f, start);
+    p.corr1 = std::min((float) (n_dims - 1), end);
+    p.freq_scale = rope->freq_scale;
+    p.ext_factor = rope->ext_factor;
+    p.mscale = rope->attn_factor;
+    if (rope->ext_factor != 0.0f) p.mscale *= 1.0f + 0.1f * logf(1.0f / rope->freq_scale);
+    const hipError_t e = launch_rope_kv_write(p, type_k, type_v, (hipStream_t) stream);
+    return e == hipSuccess ? IIAN_PA_OK : IIAN_PA_ERR_HIP;
+}
+
 int iian_pa_dequant_q8_0(void *stream, const void *pool, int64_t n_cells, const int64_t *rows_idx, int64_t n_rows,
                          int64_t row_elems, float *out) {
     if (n_rows < 0 || row_elems <= 0 || row_elems % 32 || n_cells < 0) return IIAN_PA_ERR_ARG;

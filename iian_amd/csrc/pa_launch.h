@@ -60,6 +60,23 @@ struct BatchParams {
 };
 hipError_t launch_build_batch(const BatchParams &p, hipStream_t stream);
 
+// Inputs of the fused RoPE + KV write (pa_rope.hip).
+struct RopeParams {
+    const float *k_rows;          // [T][Hkv*D] before RoPE
+    const float *v_rows;          // [T][Hkv*Dv]
+    const float *q_in;            // nullable [T][H*D]
+    float *q_out;                 // [T][H*D] when q_in is set (may equal q_in)
+    const int32_t *pos;           // [T]
+    const int64_t *slots;         // [T]
+    void *k_pool, *v_pool;
+    const float *freq_factors;    // nullable [n_dims/2]
+    int32_t *err;
+    int64_t n_cells;
+    int32_t T, H, Hkv, D, Dv, n_dims, mode;
+    float theta_scale, freq_scale, ext_factor, mscale, corr0, corr1;
+};
+hipError_t launch_rope_kv_write(const RopeParams &p, int type_k, int type_v, hipStream_t stream);
+
 // General fp32 path (pa_general.hip): any K/V types of F32, F16, Q8_0; head
 // sizes 4..512 in steps of 4; any block size.
 hipError_t launch_general(const GenParams &p, int type_k, int type_v, hipStream_t stream);

@@ -266,6 +266,66 @@ def set_rows_kv(k_pool: KVPool, v_pool: KVPool, k_rows: torch.Tensor, v_rows: to
     _lib.check("iian_pa_kv_write_kv", st)
 
 
+@dataclass
+class RopeParams:
+    """The rope arguments of ggml_rope_ext as build_rope passes them
+    (src/iian/graph.cpp:250-253).  mode: 0 = NORMAL, 2 = NEOX."""
+    n_dims: int
+    mode: int = 0
+    n_ctx_orig: int = 0
+    freq_base: float = 10000.0
+    freq_scale: float = 1.0
+    ext_factor: float = 0.0
+    attn_factor: float = 1.0
+    beta_fast: float = 32.0
+    beta_slow: float = 1.0
+    freq_factors: Optional[torch.Tensor] = None   # f32 [n_dims/2] on the device
+
+
+def rope_set_rows_kv(k_pool: KVPool, v_pool: KVPool, k_rows: torch.Tensor, v_rows: torch.Tensor,
+                     slots: torch.Tensor, pos: torch.Tensor, rope: RopeParams, n_head_kv: int,
+                     q: Optional[torch.Tensor] = None, q_out: Optional[torch.Tensor] = None,
+                     err_flag: Optional[torch.Tensor] = None) -> Optional[torch.Tensor]:
+    """build_rope on K (and q) fused with the layer's two set_rows calls
+    (src/iian/graph.cpp:250-253, 319-320), one launch: k_pool[slots[t]] <-
+    rope(k_rows[t], pos[t]), v_pool[slots[t]] <- v_rows[t], and, when q
+    ([T, H, D]) is given, q rotated into q_out (a new tensor, or q itself when
+    q_out is q).  Returns the rotated q, or None."""
+    T = k_rows.shape[0]
+    for pool, rows in ((k_pool, k_rows), (v_pool, v_rows)):
+        if rows.dtype != torch.float32 or rows.dim() != 2 or rows.shape[1] != pool.n_embd or not rows.is_cuda:
+            raise ValueError("rows must be f32 [n_tokens, n_embd] GPU tensors")
+    if v_rows.shape[0] != T or k_pool.n_cells != v_pool.n_cells:
+        raise ValueError("K and V must have the same token count and cell count")
+    if k_pool.n_embd % n_head_kv or v_pool.n_embd % n_head_kv:
+        raise ValueError("pool rows must hold n_head_kv heads")
+    if slots.dtype != torch.int64 or slots.shape != (T,) or pos.dtype != torch.int32 or pos.shape != (T,):
+        raise ValueError("slots must be int64 [T] and pos int32 [T]")
+    D = k_pool.n_embd // n_head_kv
+    H = 0
+    if q is not None:
+        if q.dtype != torch.float32 or q.dim() != 3 or q.shape[0] != T or q.shape[2] != D or not q.is_contiguous():
+            raise ValueError("q must be contiguous f32 [T, H, D]")
+        H = q.shape[1]
+        if q_out is None:
+            q_out = torch.empty_like(q)
+        elif q_out.shape != q.shape or q_out.dtype != q.dtype or not q_out.is_contiguous():
+            raise ValueError("q_out must match q")
+    ff = rope.freq_factors
+    if ff is not None and (ff.dtype != torch.float32 or ff.numel() < rope.n_dims // 2 or not ff.is_cuda):
+        raise ValueError("freq_factors must be f32 with n_dims/2 values on the GPU")
+    prm = _lib.RopeParams(rope.n_dims, rope.mode, rope.n_ctx_orig, rope.freq_base, rope.freq_scale, rope.ext_factor,
+                          rope.attn_factor, rope.beta_fast, rope.beta_slow, _ptr(ff))
+    k_rows, v_rows = k_rows.contiguous(), v_rows.contiguous()
+    st = _lib.load().iian_pa_rope_kv_write(_stream(), k_rows.data_ptr(), v_rows.data_ptr(), _ptr(q), _ptr(q_out),
+                                           pos.data_ptr(), slots.data_ptr(), T, H, n_head_kv, D,
+                                           v_pool.n_embd // n_head_kv, C.byref(prm), k_pool.data.data_ptr(),
+                                           v_pool.data.data_ptr(), k_pool.n_cells, k_pool.type, v_pool.type,
+                                           _ptr(err_flag))
+    _lib.check("iian_pa_rope_kv_write", st)
+    return q_out
+
+
 def workspace_size(n_tokens: int, n_seqs: int, n_head: int, n_head_kv: int, head_dim_v: int, max_blocks: int,
                    block_size: int) -> int:
     return int(_lib.load().iian_pa_workspace_size(n_tokens, n_seqs, n_head, n_head_kv, head_dim_v, max_blocks,

@@ -203,6 +203,36 @@ int iian_pa_build_batch(void *stream, const int32_t *block_ids, const int32_t *b
                         int32_t *seq_lens, int32_t *query_start_loc, int32_t *pos, int64_t *slots,
                         int32_t *err_flag);
 
+/* Rotary position embedding, as ggml_rope_ext takes it (ggml.h; the
+ * arguments build_rope passes, src/iian/graph.cpp:250-253). */
+typedef struct {
+    int32_t n_dims;              /* rotated values per head (n_rot): even, <= head_dim */
+    int32_t mode;                /* 0 = GGML_ROPE_TYPE_NORMAL, 2 = GGML_ROPE_TYPE_NEOX */
+    int32_t n_ctx_orig;
+    float freq_base, freq_scale, ext_factor, attn_factor, beta_fast, beta_slow;
+    const float *freq_factors;   /* device, nullable: n_dims/2 divisors (rope_freqs / LongRoPE factors) */
+} iian_pa_rope_params;
+
+/* build_rope on K (and q) fused with the layer's two set_rows calls
+ * (src/iian/graph.cpp:250-253, 319-320): in one launch, for every token t,
+ *   k_pool row slots[t] <- convert(rope(k_rows[t], pos[t])),
+ *   v_pool row slots[t] <- convert(v_rows[t]),
+ *   q_out[t] <- rope(q_in[t], pos[t])        (when q_in is non-NULL; q_out may equal q_in)
+ * k_rows f32 [n_rows][n_head_kv*head_dim], v_rows f32 [n_rows][n_head_kv*head_dim_v],
+ * q f32 [n_rows][n_head*head_dim].  rope() is ggml's CPU rope
+ * (ggml-cpu/ops.cpp:5951-6230) for modes NORMAL and NEOX: the same chain of
+ * fp32 angle products, freq factors, YaRN ramp and magnitude, the pairs
+ * rotated with each product rounded; cos and sin are the correctly rounded
+ * fp32 values of the fp32 angle, where ggml calls libm cosf / sinf (which can
+ * differ in the last bit).  Conversions, slot rules and *err_flag bit 0 as
+ * iian_pa_kv_write; q is rotated whatever the slot.  Returns
+ * IIAN_PA_ERR_UNSUPPORTED for other rope modes. */
+int iian_pa_rope_kv_write(void *stream, const float *k_rows, const float *v_rows, const float *q_in,
+                          float *q_out, const int32_t *pos, const int64_t *slots, int64_t n_rows,
+                          int32_t n_head, int32_t n_head_kv, int32_t head_dim, int32_t head_dim_v,
+                          const iian_pa_rope_params *rope, void *k_pool, void *v_pool, int64_t n_cells,
+                          int type_k, int type_v, int32_t *err_flag);
+
 /* Dequantises n_rows Q8_0 rows of row_elems values each (pool rows
  * rows_idx[i]) to f32, bit-exactly as ggml's dequantize_row_q8_0
  * (ggml-quants.c:553-567).  Rows outside [0, n_cells) produce zeros.

@@ -47,6 +47,14 @@ def lib() -> C.CDLL:
             getattr(L, n).argtypes = [P, P, I64]
         L.pao_set_rows.restype = C.c_int
         L.pao_set_rows.argtypes = [P, I64, I64, P, P, I64, C.c_int]
+        L.pao_rope_cache.restype = None
+        L.pao_rope_cache.argtypes = [I32, C.c_int, C.c_int, C.c_float, C.c_float, C.c_float, C.c_float, C.c_float,
+                                     C.c_float, P, P]
+        L.pao_rope_rows.restype = C.c_int
+        L.pao_rope_rows.argtypes = [P, P, I64, C.c_int, C.c_int, P, C.c_int, C.c_int, C.c_int, C.c_float, C.c_float,
+                                    C.c_float, C.c_float, C.c_float, C.c_float, P]
+        L.pao_rope_corr_dims.restype = None
+        L.pao_rope_corr_dims.argtypes = [C.c_int, C.c_int, C.c_float, C.c_float, C.c_float, P]
         L.pao_build_batch.restype = C.c_int64
         L.pao_build_batch.argtypes = [P, P, P, P, I32, I32, I32, P, P, P, P, P, P, P]
         L.pao_paged_attention.restype = C.c_int
@@ -175,3 +183,37 @@ def build_batch(block_ids, num_computed, n_new, block_size: int, max_blocks: int
         raise ValueError("pao_build_batch rejected its arguments")
     return dict(block_tables=bt, seq_lens=sl, query_start_loc=qsl, pos=pos[:T], slots=slots[:T],
                 seq_idx=seq_idx[:T], cells=np.split(cells[:int(L.sum())], np.cumsum(L)[:-1]))
+
+
+def rope_cache(pos: int, n_dims: int, n_ctx_orig: int = 0, freq_base: float = 10000.0, freq_scale: float = 1.0,
+               ext_factor: float = 0.0, attn_factor: float = 1.0, beta_fast: float = 32.0, beta_slow: float = 1.0,
+               freq_factors: Optional[np.ndarray] = None) -> np.ndarray:
+    """(cos, sin) per pair of one position (pa_oracle.c pao_rope_cache)."""
+    out = np.empty(n_dims, np.float32)
+    ff = None if freq_factors is None else np.ascontiguousarray(freq_factors, dtype=np.float32)
+    lib().pao_rope_cache(int(pos), n_dims, n_ctx_orig, freq_base, freq_scale, ext_factor, attn_factor, beta_fast,
+                         beta_slow, None if ff is None else _p(ff), _p(out))
+    return out
+
+
+def rope_rows(x: np.ndarray, pos: np.ndarray, n_heads: int, head_dim: int, n_dims: int, mode: int = 0,
+              n_ctx_orig: int = 0, freq_base: float = 10000.0, freq_scale: float = 1.0, ext_factor: float = 0.0,
+              attn_factor: float = 1.0, beta_fast: float = 32.0, beta_slow: float = 1.0,
+              freq_factors: Optional[np.ndarray] = None) -> np.ndarray:
+    """ggml_rope_ext forward on f32 rows [T, n_heads*head_dim] (pao_rope_rows)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    ps = np.ascontiguousarray(pos, dtype=np.int32)
+    ff = None if freq_factors is None else np.ascontiguousarray(freq_factors, dtype=np.float32)
+    st = lib().pao_rope_rows(_p(x), _p(y), x.shape[0], n_heads, head_dim, _p(ps), n_dims, mode, n_ctx_orig,
+                             freq_base, freq_scale, ext_factor, attn_factor, beta_fast, beta_slow,
+                             None if ff is None else _p(ff))
+    if st != 0:
+        raise ValueError("pao_rope_rows rejected its arguments")
+    return y
+
+
+def rope_corr_dims(n_dims: int, n_ctx_orig: int, freq_base: float, beta_fast: float, beta_slow: float):
+    out = np.empty(2, np.float32)
+    lib().pao_rope_corr_dims(n_dims, n_ctx_orig, freq_base, beta_fast, beta_slow, _p(out))
+    return out

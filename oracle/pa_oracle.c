@@ -383,3 +383,96 @@ int64_t pao_build_batch(const int32_t *block_ids, const int32_t *block_off, cons
     }
     return T;
 }
+
+/* ------------------------------------------------------------------ RoPE */
+
+/* ggml_rope_yarn_corr_dims (ggml.c:4418-4430): the dims where YaRN's ramp
+ * starts and ends. */
+static float rope_yarn_corr_dim(int n_dims, int n_ctx_orig, float n_rot, float base) {
+    return n_dims * logf(n_ctx_orig / (n_rot * 2 * (float) M_PI)) / (2 * logf(base));
+}
+
+void pao_rope_corr_dims(int n_dims, int n_ctx_orig, float freq_base, float beta_fast, float beta_slow,
+                        float dims[2]) {
+    const float start = floorf(rope_yarn_corr_dim(n_dims, n_ctx_orig, beta_fast, freq_base));
+    const float end = ceilf(rope_yarn_corr_dim(n_dims, n_ctx_orig, beta_slow, freq_base));
+    dims[0] = start > 0 ? start : 0;
+    dims[1] = end < n_dims - 1 ? end : (float) (n_dims - 1);
+}
+
+/* rope_yarn_ramp (ggml-cpu/ops.cpp:5951-5954). */
+static float rope_yarn_ramp(float low, float high, int i0) {
+    const float den = high - low > 0.001f ? high - low : 0.001f;
+    const float y = (i0 / 2 - low) / den;
+    return 1 - (y < 0 ? 0 : (y > 1 ? 1 : y));
+}
+
+/* The (cos, sin) cache of one position: ggml_rope_cache_init + rope_yarn
+ * (ggml-cpu/ops.cpp:5958-5990): theta starts at the position and is multiplied
+ * by theta_scale = powf(freq_base, -2/n_dims) once per pair; each pair's angle
+ * is theta / freq_factor, interpolated by freq_scale and, with ext_factor != 0,
+ * mixed by the YaRN ramp; the magnitude is attn_factor, times
+ * 1 + 0.1 ln(1/freq_scale) with ext_factor != 0.  cos and sin are the
+ * correctly rounded fp32 values of the fp32 angle (evaluated in fp64); ggml
+ * calls libm cosf / sinf, which differ from those in the last bit on a small
+ * fraction of angles (measured in tests/test_oracle.py).  Arithmetic is the
+ * C source's, without fused multiply-adds (the oracle is built with
+ * -ffp-contract=off).  cache holds n_dims floats: cos, sin per pair. */
+void pao_rope_cache(int32_t pos, int n_dims, int n_ctx_orig, float freq_base, float freq_scale, float ext_factor,
+                    float attn_factor, float beta_fast, float beta_slow, const float *freq_factors, float *cache) {
+    const float theta_scale = powf(freq_base, -2.0f / n_dims);
+    float corr[2];
+    pao_rope_corr_dims(n_dims, n_ctx_orig, freq_base, beta_fast, beta_slow, corr);
+    float theta = (float) pos;
+    for (int i0 = 0; i0 < n_dims; i0 += 2) {
+        const float ff = freq_factors ? freq_factors[i0 / 2] : 1.0f;
+        const float theta_extrap = theta / ff;
+        const float theta_interp = freq_scale * theta_extrap;
+        float th = theta_interp, mscale = attn_factor;
+        if (ext_factor != 0.0f) {
+            const float ramp_mix = rope_yarn_ramp(corr[0], corr[1], i0) * ext_factor;
+            th = theta_interp * (1 - ramp_mix) + theta_extrap * ramp_mix;
+            mscale *= 1.0f + 0.1f * logf(1.0f / freq_scale);
+        }
+        cache[i0 + 0] = (float) cos((double) th) * mscale;
+        cache[i0 + 1] = (float) sin((double) th) * mscale;
+        theta *= theta_scale;
+    }
+}
+
+/* ggml_rope_ext forward on f32 rows (ggml_compute_forward_rope_flt,
+ * ggml-cpu/ops.cpp:6082-6230; rotate_pairs :6063-6080): each row holds
+ * n_heads heads of head_dim values at position pos[row]; the first n_dims
+ * values of each head are rotated in pairs (NORMAL, mode 0: (2i, 2i+1);
+ * NEOX, mode 2: (i, i + n_dims/2)), y0 = x0 c - x1 s, y1 = x0 s + x1 c, and
+ * the rest are copied.  x and y may be the same array.  Returns 0, or -1 for
+ * an unsupported mode or n_dims (odd, or above head_dim). */
+int pao_rope_rows(const float *x, float *y, int64_t n_rows, int n_heads, int head_dim, const int32_t *pos,
+                  int n_dims, int mode, int n_ctx_orig, float freq_base, float freq_scale, float ext_factor,
+                  float attn_factor, float beta_fast, float beta_slow, const float *freq_factors) {
+    if ((mode != 0 && mode != 2) || n_dims <= 0 || n_dims % 2 || n_dims > head_dim) return -1;
+    float *cache = (float *) malloc(sizeof(float) * (size_t) n_dims);
+    if (!cache) return -1;
+    for (int64_t r = 0; r < n_rows; r++) {
+        pao_rope_cache(pos[r], n_dims, n_ctx_orig, freq_base, freq_scale, ext_factor, attn_factor, beta_fast,
+                       beta_slow, freq_factors, cache);
+        for (int h = 0; h < n_heads; h++) {
+            const float *src = x + (r * n_heads + h) * (int64_t) head_dim;
+            float *dst = y + (r * n_heads + h) * (int64_t) head_dim;
+            float tmp[1024];
+            const float *s = src;
+            if (src == dst) { memcpy(tmp, src, sizeof(float) * (size_t) head_dim); s = tmp; }
+            for (int i0 = 0; i0 < n_dims; i0 += 2) {
+                const int e0 = mode == 0 ? i0 : i0 / 2;
+                const int e1 = mode == 0 ? i0 + 1 : i0 / 2 + n_dims / 2;
+                const float c = cache[i0], sn = cache[i0 + 1];
+                const float x0 = s[e0], x1 = s[e1];
+                dst[e0] = x0 * c - x1 * sn;
+                dst[e1] = x0 * sn + x1 * c;
+            }
+            for (int i = n_dims; i < head_dim; i++) dst[i] = s[i];
+        }
+    }
+    free(cache);
+    return 0;
+}

@@ -98,6 +98,19 @@ int64_t pao_build_batch(const int32_t *block_ids, const int32_t *block_off, cons
                         int32_t *block_tables, int32_t *seq_lens, int32_t *qsl, int32_t *pos, int64_t *slots,
                         int32_t *seq_idx, int64_t *cells);
 
+/* RoPE as ggml_rope_ext computes it on the CPU (ggml-cpu/ops.cpp:5951-6230,
+ * ggml.c:4418-4430), modes NORMAL (0) and NEOX (2); see pa_oracle.c for the
+ * cos/sin evaluation.  pao_rope_cache writes the n_dims (cos, sin) values of
+ * one position; pao_rope_rows rotates rows of n_heads heads (x may equal y);
+ * pao_rope_corr_dims is ggml_rope_yarn_corr_dims. */
+void pao_rope_corr_dims(int n_dims, int n_ctx_orig, float freq_base, float beta_fast, float beta_slow,
+                        float dims[2]);
+void pao_rope_cache(int32_t pos, int n_dims, int n_ctx_orig, float freq_base, float freq_scale, float ext_factor,
+                    float attn_factor, float beta_fast, float beta_slow, const float *freq_factors, float *cache);
+int pao_rope_rows(const float *x, float *y, int64_t n_rows, int n_heads, int head_dim, const int32_t *pos,
+                  int n_dims, int mode, int n_ctx_orig, float freq_base, float freq_scale, float ext_factor,
+                  float attn_factor, float beta_fast, float beta_slow, const float *freq_factors);
+
 #ifdef __cplusplus
 }
 #endif

@@ -332,3 +332,111 @@ def test_build_batch_rejects_short_block_lists(oracle):
         oracle.build_batch([[3, 4], [5]], [20, 0], [20, 1], 16, 4)   # 40 tokens in 2 blocks of 16
     with pytest.raises(ValueError):
         oracle.build_batch([[3, 4, 5]], [0], [40], 16, 2)            # more blocks than the table row holds
+
+
+# ---------------------------------------------------------------- RoPE
+
+def _theta_exact(pos, n_dims, base, freq_scale=1.0, ff=None):
+    i = np.arange(n_dims // 2, dtype=np.float64)
+    th = pos * np.power(np.float64(base), -2.0 * i / n_dims)
+    if ff is not None:
+        th = th / np.asarray(ff, np.float64)
+    return th * freq_scale
+
+
+@pytest.mark.parametrize("base,pos", [(10000.0, 0), (10000.0, 1), (10000.0, 1000), (500000.0, 8191),
+                                      (1e6, 32767), (10000.0, 65535)])
+def test_rope_cache_closed_form(oracle, base, pos):
+    """cos/sin of pos * base^(-2i/n_dims) (the rope closed form), within the
+    error of ggml's fp32 angle chain: after i products the angle carries a
+    relative error below (2i + 2) * 2^-24."""
+    n_dims = 128
+    c = oracle.rope_cache(pos, n_dims, freq_base=base).reshape(-1, 2)
+    th = _theta_exact(pos, n_dims, base)
+    bound = th * (2 * np.arange(n_dims // 2) + 2) * 2.0 ** -24 + 2.0 ** -23
+    assert (np.abs(c[:, 0] - np.cos(th)) <= bound).all()
+    assert (np.abs(c[:, 1] - np.sin(th)) <= bound).all()
+    if pos == 0:
+        assert (c[:, 0] == 1).all() and (c[:, 1] == 0).all()
+
+
+def test_rope_freq_factors_scale_and_magnitude(oracle):
+    """freq factors divide each pair's angle, freq_scale multiplies it, and
+    attn_factor is the magnitude (LongRoPE / linear scaling / mscale)."""
+    rng = np.random.default_rng(11)
+    ff = rng.uniform(1.0, 40.0, 48).astype(np.float32)
+    c = oracle.rope_cache(3000, 96, freq_base=10000.0, freq_scale=0.5, attn_factor=1.25, freq_factors=ff).reshape(-1, 2)
+    th = _theta_exact(3000, 96, 10000.0, 0.5, ff)
+    bound = 3000 * (2 * np.arange(48) + 4) * 2.0 ** -24 + 2.0 ** -22
+    assert (np.abs(c[:, 0] - 1.25 * np.cos(th)) <= bound).all()
+    assert (np.abs(c[:, 1] - 1.25 * np.sin(th)) <= bound).all()
+
+
+def test_rope_yarn_ramp_ends(oracle):
+    """YaRN (ext_factor = 1): pairs below the first correction dim keep the
+    extrapolated angle, pairs past the second take the interpolated one
+    (freq_scale times it), and the magnitude is attn_factor * (1 + 0.1 ln(1/s))
+    (ggml-cpu/ops.cpp:5958-5973, ggml.c:4418-4430)."""
+    n_dims, n_ctx, base, fs = 128, 4096, 10000.0, 0.25
+    lo, hi = oracle.rope_corr_dims(n_dims, n_ctx, base, 32.0, 1.0)
+    corr = lambda beta: n_dims * np.log(n_ctx / (beta * 2 * np.pi)) / (2 * np.log(base))
+    assert lo == max(0.0, np.floor(corr(32.0))) and hi == min(n_dims - 1, np.ceil(corr(1.0)))
+    c = oracle.rope_cache(2000, n_dims, n_ctx_orig=n_ctx, freq_base=base, freq_scale=fs, ext_factor=1.0).reshape(-1, 2)
+    th = _theta_exact(2000, n_dims, base)
+    m = 1.0 + 0.1 * np.log(1.0 / fs)
+    i = np.arange(n_dims // 2)
+    bound = 2000 * (2 * i + 4) * 2.0 ** -24 + 2.0 ** -21
+    below, above = i < lo, i > hi
+    assert below.any() and above.any()
+    assert (np.abs(c[below, 0] - m * np.cos(th[below])) <= bound[below]).all()
+    assert (np.abs(c[above, 0] - m * np.cos(fs * th[above])) <= bound[above]).all()
+
+
+@pytest.mark.parametrize("mode", [0, 2])
+def test_rope_rows_pairs_and_invariants(oracle, mode):
+    """NORMAL rotates (2i, 2i+1) and NEOX (i, i + n_dims/2) by the pair's
+    angle: NEOX on x equals NORMAL on x with its halves interleaved; each
+    pair's norm is kept (attn_factor 1); dims past n_dims are copied; position
+    0 is the identity."""
+    rng = np.random.default_rng(12 + mode)
+    T, Hh, D, nd = 9, 3, 128, 64
+    x = rng.standard_normal((T, Hh * D)).astype(np.float32)
+    pos = rng.integers(0, 5000, T).astype(np.int32)
+    pos[0] = 0
+    y = oracle.rope_rows(x, pos, Hh, D, nd, mode=mode, freq_base=10000.0)
+    xs, ys = x.reshape(T, Hh, D), y.reshape(T, Hh, D)
+    assert np.array_equal(ys[:, :, nd:], xs[:, :, nd:])
+    assert np.array_equal(ys[0], xs[0])
+    e0 = np.arange(0, nd, 2) if mode == 0 else np.arange(nd // 2)
+    e1 = e0 + 1 if mode == 0 else e0 + nd // 2
+    n_in = xs[:, :, e0].astype(np.float64) ** 2 + xs[:, :, e1].astype(np.float64) ** 2
+    n_out = ys[:, :, e0].astype(np.float64) ** 2 + ys[:, :, e1].astype(np.float64) ** 2
+    assert np.allclose(n_in, n_out, rtol=1e-5, atol=1e-6)
+    if mode == 2:   # NEOX == NORMAL on interleaved halves
+        perm = np.empty(nd, np.int64)
+        perm[0::2], perm[1::2] = np.arange(nd // 2), np.arange(nd // 2) + nd // 2
+        xi = xs.copy()
+        xi[:, :, :nd] = xs[:, :, perm]
+        yn = oracle.rope_rows(xi.reshape(T, -1), pos, Hh, D, nd, mode=0, freq_base=10000.0).reshape(T, Hh, D)
+        back = np.empty_like(yn)
+        back[:, :, perm] = yn[:, :, :nd]
+        assert np.array_equal(back[:, :, :nd], ys[:, :, :nd])
+
+
+def test_rope_cos_sin_against_libm(oracle):
+    """The oracle's cos/sin are the correctly rounded values of the fp32 angle;
+    glibc's cosf/sinf (what ggml calls) agree with them on all but a small
+    fraction of angles, and then by one unit in the last place."""
+    import ctypes
+    libm = ctypes.CDLL("libm.so.6")
+    libm.cosf.restype = libm.sinf.restype = ctypes.c_float
+    libm.cosf.argtypes = libm.sinf.argtypes = [ctypes.c_float]
+    rng = np.random.default_rng(13)
+    th = rng.uniform(0, 30000, 20000).astype(np.float32)
+    cr = np.cos(th.astype(np.float64)).astype(np.float32)
+    lm = np.array([libm.cosf(float(t)) for t in th], np.float32)
+    diff = np.abs(cr.view(np.int32).astype(np.int64) - lm.view(np.int32).astype(np.int64))
+    assert diff.max() <= 1
+    assert (diff != 0).mean() < 0.02
+    c = oracle.rope_cache(1, 2, freq_base=10000.0)   # angle 1.0 exactly
+    assert c[0] == np.float32(np.cos(1.0)) and c[1] == np.float32(np.sin(1.0))
