@@ -11,6 +11,7 @@ from .paged_attn import (  # noqa: F401
     GGML_TYPE_Q8_0,
     KVPool,
     PagedAttnParams,
+    PagedAttnRuntime,
     PagedBatch,
     RequestBlocks,
     RopeParams,
@@ -23,6 +24,7 @@ from .paged_attn import (  # noqa: F401
     row_bytes,
     set_rows,
     set_rows_kv,
+    swa_free_blocks,
     workspace_size,
 )
 from ._lib import PagedAttnError  # noqa: F401

@@ -40,10 +40,23 @@ SIGNATURES = {
                                             _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32,
                                             C.c_float, C.c_float, _I32, _I32, _P, _P]),
     "iian_pa_build_batch": (C.c_int, [_P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P]),
+    "iian_pa_swa_free_blocks": (C.c_int, [_P, _P, _P, _I32, _I32, _I32, _I32, _P, _P, _I32]),
     "iian_pa_rope_kv_write": (C.c_int, [_P, _P, _P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _I32, _P, _P, _P, _I64,
                                         C.c_int, C.c_int, _P]),
+    "iian_pa_runtime_create": (C.c_int, [_P, _P]),
+    "iian_pa_runtime_destroy": (None, [_P]),
+    "iian_pa_runtime_begin_step": (C.c_int, [_P, _P, _P, _P, _P, _P, _I32]),
+    "iian_pa_runtime_layer": (C.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, C.c_float, C.c_float, _I32, _I32, _P]),
+    "iian_pa_runtime_errors": (C.c_int, [_P, _P, _P]),
     "iian_pa_dequant_q8_0": (C.c_int, [_P, _P, _I64, _P, _I64, _I64, _P]),
 }
+
+
+class RuntimeConfig(C.Structure):
+    """iian_pa_runtime_config of include/iian_pa.h."""
+    _fields_ = [(n, C.c_int32) for n in ("max_seqs", "max_tokens", "max_blocks_per_seq", "max_total_blocks",
+                                         "n_head", "n_head_kv", "head_dim", "head_dim_v", "block_size", "num_blocks",
+                                         "type_k", "type_v")]
 
 
 class RopeParams(C.Structure):

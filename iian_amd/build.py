@@ -19,7 +19,7 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libiian_pa.so"
 SOURCES = ["pa_abi.hip", "pa_decode.hip", "pa_decode_q8.hip", "pa_prefill.hip", "pa_prefill16.hip", "pa_general.hip",
-           "pa_kv_write.hip", "pa_batch.hip", "pa_rope.hip"]
+           "pa_kv_write.hip", "pa_batch.hip", "pa_rope.hip", "pa_runtime.hip"]
 ARCH = "gfx950"
 
 # Packed-FP32 VALU ops are disabled for all device code: some of their forms

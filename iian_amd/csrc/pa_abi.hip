@@ -536,6 +536,18 @@ int iian_pa_build_batch(void *stream, const int32_t *block_ids, const int32_t *b
     return launch_build_batch(p, (hipStream_t) stream) == hipSuccess ? IIAN_PA_OK : IIAN_PA_ERR_HIP;
 }
 
+int iian_pa_swa_free_blocks(void *stream, const int32_t *query_start_loc, const int32_t *pos, int32_t n_seqs,
+                            int32_t n_tokens, int32_t n_swa, int32_t block_size, int32_t *n_free,
+                            int32_t *block_tables, int32_t max_blocks) {
+    if (n_seqs < 0 || n_tokens < 0 || n_swa < 0 || block_size <= 0 || (block_tables && max_blocks <= 0))
+        return IIAN_PA_ERR_ARG;
+    if (n_seqs == 0) return IIAN_PA_OK;
+    if (!query_start_loc || !n_free || (n_tokens > 0 && !pos)) return IIAN_PA_ERR_NULL;
+    const hipError_t e = launch_swa_free(query_start_loc, pos, n_seqs, n_tokens, n_swa, block_size, n_free,
+                                         block_tables, max_blocks, (hipStream_t) stream);
+    return e == hipSuccess ? IIAN_PA_OK : IIAN_PA_ERR_HIP;
+}
+
 int iian_pa_rope_kv_write(void *stream, const float *k_rows, const float *v_rows, const float *q_in, float *q_out,
                           const int32_t *pos, const int64_t *slots, int64_t n_rows, int32_t n_head, int32_t n_head_kv,
                           int32_t head_dim, int32_t head_dim_v, const iian_pa_rope_params *rope, void *k_pool,

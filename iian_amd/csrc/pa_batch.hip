@@ -74,6 +74,41 @@ __global__ __launch_bounds__(256) void pa_build_batch_kernel(BatchParams p) {
     }
 }
 
+// Sliding-window block freeing (the reference's planned "free out-of-window
+// blocks", docs/ROADMAP.md:33).  On a layer with window n_swa, a query at
+// position q sees cells c > q - n_swa (src/iian/paged_attn.cpp:124), and the
+// kernels start reading at that bound rounded down to a multiple of kTile.
+// A sequence's later steps only have larger positions, so every block that
+// ends at or before align_down(min_pos - n_swa + 1, kTile) is never read again
+// by any kernel of this library: n_free[s] counts those leading blocks, and
+// their table entries may be overwritten (with -1 here) and the blocks
+// reused.  One wave per sequence.
+__global__ __launch_bounds__(256) void pa_swa_free_kernel(const int32_t *__restrict__ qsl,
+                                                          const int32_t *__restrict__ pos, int32_t S, int32_t T,
+                                                          int32_t n_swa, int32_t block_size, int32_t *n_free,
+                                                          int32_t *block_tables, int32_t max_blocks) {
+    const int s = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (s >= S) return;
+    const int q0 = min(max(qsl[s], 0), T), q1 = min(max(qsl[s + 1], q0), T);
+    int mn = INT32_MAX;
+    for (int t = q0 + lane; t < q1; t += 64) mn = min(mn, pos[t]);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) mn = min(mn, __shfl_xor(mn, o));
+    int nf = 0;
+    if (q1 > q0 && n_swa > 0) nf = (max(0, mn - n_swa + 1) & ~(kTile - 1)) / block_size;
+    if (lane == 0) n_free[s] = nf;
+    if (block_tables)
+        for (int b = lane; b < min(nf, max_blocks); b += 64) block_tables[(int64_t) s * max_blocks + b] = -1;
+}
+
+hipError_t launch_swa_free(const int32_t *qsl, const int32_t *pos, int32_t S, int32_t T, int32_t n_swa,
+                           int32_t block_size, int32_t *n_free, int32_t *block_tables, int32_t max_blocks,
+                           hipStream_t stream) {
+    hipLaunchKernelGGL(pa_swa_free_kernel, dim3((S + 3) / 4), dim3(256), 0, stream, qsl, pos, S, T, n_swa, block_size,
+                       n_free, block_tables, max_blocks);
+    return hipGetLastError();
+}
+
 hipError_t launch_build_batch(const BatchParams &p, hipStream_t stream) {
     hipLaunchKernelGGL(pa_build_batch_kernel, dim3(p.S), dim3(256), 0, stream, p);
     return hipGetLastError();

@@ -59,6 +59,9 @@ struct BatchParams {
     int32_t S, T, block_size, max_blocks, num_blocks;
 };
 hipError_t launch_build_batch(const BatchParams &p, hipStream_t stream);
+hipError_t launch_swa_free(const int32_t *qsl, const int32_t *pos, int32_t S, int32_t T, int32_t n_swa,
+                           int32_t block_size, int32_t *n_free, int32_t *block_tables, int32_t max_blocks,
+                           hipStream_t stream);
 
 // Inputs of the fused RoPE + KV write (pa_rope.hip).
 struct RopeParams {

@@ -224,6 +224,89 @@ def build_batch(req: RequestBlocks, n_tokens: int, block_size: int, max_blocks: 
     return out
 
 
+def swa_free_blocks(batch: PagedBatch, n_swa: int, clear_table: bool = False) -> torch.Tensor:
+    """Per sequence, the leading blocks a sliding-window layer (window n_swa)
+    will never read again at this step or later (the reference's planned
+    out-of-window block freeing, docs/ROADMAP.md:33): int32 [S].  With
+    clear_table, those block-table entries are set to -1."""
+    S = batch.n_seqs
+    dev = batch.pos.device
+    _check_batch(batch, dev)
+    n_free = torch.empty(S, dtype=torch.int32, device=dev)
+    st = _lib.load().iian_pa_swa_free_blocks(_stream(), batch.query_start_loc.data_ptr(), batch.pos.data_ptr(), S,
+                                             batch.n_tokens, int(n_swa), batch.block_size, n_free.data_ptr(),
+                                             batch.block_tables.data_ptr() if clear_table else None,
+                                             int(batch.block_tables.shape[1]))
+    _lib.check("iian_pa_swa_free_blocks", st)
+    return n_free
+
+
+class PagedAttnRuntime:
+    """The engine-side runtime (iian_pa_runtime_*): device buffers of one
+    step allocated once; begin_step per engine step from the scheduler's
+    per-request block ids and counts, layer per attention layer.  Replaces the
+    host UBatch expansion of Engine::step (src/iian/engine.cpp:491-535) and
+    the paged branch of build_attn (src/iian/graph.cpp:314-337)."""
+
+    def __init__(self, max_seqs: int, max_tokens: int, max_blocks_per_seq: int, max_total_blocks: int, n_head: int,
+                 n_head_kv: int, head_dim: int, head_dim_v: int, block_size: int, num_blocks: int, type_k: int,
+                 type_v: int):
+        self._lib = _lib.load()
+        self.cfg = _lib.RuntimeConfig(max_seqs, max_tokens, max_blocks_per_seq, max_total_blocks, n_head, n_head_kv,
+                                      head_dim, head_dim_v, block_size, num_blocks, type_k, type_v)
+        h = C.c_void_p()
+        _lib.check("iian_pa_runtime_create", self._lib.iian_pa_runtime_create(C.byref(self.cfg), C.byref(h)))
+        self._h = h
+
+    def close(self) -> None:
+        if self._h:
+            self._lib.iian_pa_runtime_destroy(self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def begin_step(self, block_ids: Sequence[Sequence[int]], num_computed: Sequence[int],
+                   n_new: Sequence[int]) -> None:
+        S = len(block_ids)
+        arrs = [np.ascontiguousarray(b, dtype=np.int32) for b in block_ids]
+        ptrs = (C.c_void_p * max(S, 1))(*[a.ctypes.data if a.size else None for a in arrs])
+        nb = np.array([a.size for a in arrs], np.int32)
+        nc = np.ascontiguousarray(num_computed, dtype=np.int32)
+        nn = np.ascontiguousarray(n_new, dtype=np.int32)
+        st = self._lib.iian_pa_runtime_begin_step(self._h, _stream(), ptrs, nb.ctypes.data, nc.ctypes.data,
+                                                  nn.ctypes.data, S)
+        _lib.check("iian_pa_runtime_begin_step", st)
+
+    def layer(self, q: torch.Tensor, k_rows: torch.Tensor, v_rows: torch.Tensor, k_pool: KVPool, v_pool: KVPool,
+              params: PagedAttnParams, out: torch.Tensor, rope: Optional[RopeParams] = None,
+              q_rot: Optional[torch.Tensor] = None) -> None:
+        for t in (q, k_rows, v_rows, out):
+            if t.dtype != torch.float32 or not t.is_contiguous() or not t.is_cuda:
+                raise ValueError("q, k_rows, v_rows and out must be contiguous f32 GPU tensors")
+        prm = None
+        if rope is not None:
+            if q_rot is None:
+                raise ValueError("rope needs q_rot (q itself for an in-place rotation)")
+            prm = _lib.RopeParams(rope.n_dims, rope.mode, rope.n_ctx_orig, rope.freq_base, rope.freq_scale,
+                                  rope.ext_factor, rope.attn_factor, rope.beta_fast, rope.beta_slow,
+                                  _ptr(rope.freq_factors))
+        st = self._lib.iian_pa_runtime_layer(self._h, _stream(), q.data_ptr(), _ptr(q_rot), k_rows.data_ptr(),
+                                             v_rows.data_ptr(), C.byref(prm) if prm is not None else None,
+                                             k_pool.data.data_ptr(), v_pool.data.data_ptr(), float(params.scale),
+                                             float(params.softcap), int(bool(params.causal)), int(params.n_swa),
+                                             out.data_ptr())
+        _lib.check("iian_pa_runtime_layer", st)
+
+    def errors(self) -> int:
+        e = C.c_int32(0)
+        _lib.check("iian_pa_runtime_errors", self._lib.iian_pa_runtime_errors(self._h, _stream(), C.byref(e)))
+        return int(e.value)
+
+
 def paged_attn_supported(type_k: int, type_v: int, max_alibi_bias: float, head_dim: int = 128,
                          head_dim_v: Optional[int] = None) -> bool:
     """src/iian/paged_attn.cpp:15-18, as supported by the gfx950 kernels."""

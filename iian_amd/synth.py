@@ -168,12 +168,24 @@ def _fill_randn(dst: torch.Tensor, gen: torch.Generator, chunk: int = 1 << 26) -
         flat[i:i + n] = torch.randn(n, generator=gen, device=dst.device, dtype=torch.float32).to(torch.float16)
 
 
-def build(sp: Spec, device: str = "cuda") -> Workload:
+def build(sp: Spec, device: str = "cuda", replicas: int = 1) -> Workload:
     """Materialise the workload on `device`: metadata from numpy's seeded
-    generator, tensor values from torch's seeded generator on that device."""
+    generator, tensor values from torch's seeded generator on that device.
+    With replicas > 1 the pool holds that many disjoint copies of the
+    workload's blocks (pool blocks r*num_blocks + id), each with its own
+    values, and Workload.extra['replica_batches'] holds one batch per copy:
+    cycling through them keeps a small workload's KV out of the caches
+    between steps."""
     rng = np.random.default_rng(sp.seed + 1000)
     bs = sp.block_size
     bt = _tables(sp, rng)
+    if replicas > 1:
+        sp = Spec(**{**sp.__dict__, "num_blocks": sp.num_blocks * replicas})
+        used0 = bt >= 0
+        base_num = sp.num_blocks // replicas
+        bt_all = [np.where(used0, bt + r * base_num, -1).astype(np.int32) for r in range(replicas)]
+    else:
+        bt_all = [bt]
     S = len(sp.seq_lens)
     seq_idx, pos, slots = [], [], []
     for s in range(S):
@@ -197,7 +209,7 @@ def build(sp: Spec, device: str = "cuda") -> Workload:
     n_cells = sp.num_blocks * bs
     k_pool = KVPool(n_cells, n_embd, sp.kv_type, device=device)
     v_pool = KVPool(n_cells, n_embd, sp.kv_type, device=device)
-    used = np.unique(bt[bt >= 0]).astype(np.int64)
+    used = np.unique(np.concatenate([b[b >= 0] for b in bt_all])).astype(np.int64)
     used_t = torch.as_tensor(used, device=device)
     if sp.kv_type == GGML_TYPE_F16:
         for pool in (k_pool, v_pool):
@@ -219,7 +231,15 @@ def build(sp: Spec, device: str = "cuda") -> Workload:
         query_start_loc=torch.as_tensor(qsl, device=device), pos=torch.as_tensor(pos, device=device),
         slots=torch.as_tensor(slots, device=device), max_query_len=int(sp.n_q.max()), block_size=bs)
     params = PagedAttnParams(scale=sp.scale, softcap=sp.softcap, causal=True, n_swa=sp.n_swa)
-    return Workload(sp, bt, seq_idx, pos, slots, qsl, params, q, k_new, v_new, k_pool, v_pool, batch)
+    w = Workload(sp, bt, seq_idx, pos, slots, qsl, params, q, k_new, v_new, k_pool, v_pool, batch)
+    if replicas > 1:
+        w.extra["replica_batches"] = [batch] + [
+            PagedBatch(block_tables=torch.as_tensor(b, device=device), seq_lens=batch.seq_lens,
+                       query_start_loc=batch.query_start_loc, pos=batch.pos,
+                       slots=torch.as_tensor(slots + (r + 1) * (sp.num_blocks // replicas) * bs, device=device),
+                       max_query_len=batch.max_query_len, block_size=bs)
+            for r, b in enumerate(bt_all[1:])]
+    return w
 
 
 def attended_cells(sp: Spec, pos: np.ndarray, seq_idx: np.ndarray) -> np.ndarray:

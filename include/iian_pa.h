@@ -203,6 +203,23 @@ int iian_pa_build_batch(void *stream, const int32_t *block_ids, const int32_t *b
                         int32_t *seq_lens, int32_t *query_start_loc, int32_t *pos, int64_t *slots,
                         int32_t *err_flag);
 
+/* Sliding-window block freeing, the reference's planned "free out-of-window
+ * blocks" (docs/ROADMAP.md:33), for a layer with window n_swa > 0: writes to
+ * n_free[s] (int32 [S]) the number of leading blocks of sequence s that no
+ * query of this step, and none of a later step (whose positions are larger),
+ * can see: the blocks that end at or before
+ * align_down(min_pos_s - n_swa + 1, 32), where min_pos_s is the smallest
+ * position of the sequence's tokens in pos[query_start_loc[s] ..
+ * query_start_loc[s+1]).  No attention kernel of this library reads those
+ * blocks again (the kernels start a window at that 32-cell boundary), so the
+ * block manager may release them from a pool that only sliding-window layers
+ * use; their table entries may then hold anything.  When block_tables is
+ * non-NULL (int32 [S][max_blocks]), those entries are overwritten with -1.
+ * n_swa == 0 (a global layer) frees nothing. */
+int iian_pa_swa_free_blocks(void *stream, const int32_t *query_start_loc, const int32_t *pos, int32_t n_seqs,
+                            int32_t n_tokens, int32_t n_swa, int32_t block_size, int32_t *n_free,
+                            int32_t *block_tables, int32_t max_blocks);
+
 /* Rotary position embedding, as ggml_rope_ext takes it (ggml.h; the
  * arguments build_rope passes, src/iian/graph.cpp:250-253). */
 typedef struct {
@@ -232,6 +249,61 @@ int iian_pa_rope_kv_write(void *stream, const float *k_rows, const float *v_rows
                           int32_t n_head, int32_t n_head_kv, int32_t head_dim, int32_t head_dim_v,
                           const iian_pa_rope_params *rope, void *k_pool, void *v_pool, int64_t n_cells,
                           int type_k, int type_v, int32_t *err_flag);
+
+/* ---- Engine runtime: the integration point for an engine with its KV cache on the GPU ----
+ *
+ * Replaces, on the GPU, the step-level work around the paged op: the host
+ * UBatch cell expansion of Engine::step (src/iian/engine.cpp:491-535) and the
+ * paged branch of GraphContext::build_attn (src/iian/graph.cpp:314-337), which
+ * the reference runs on the CPU only (engine.cpp:187-188; its GPU path
+ * gathers K/V instead, graph.cpp:487-518).  A runtime owns one step's device
+ * buffers (request state, block tables, seq_lens, query_start_loc, pos,
+ * slots, attention workspace, error word) and a double-buffered pinned
+ * staging area, all allocated by iian_pa_runtime_create for the configured
+ * maxima; nothing is allocated afterwards.  One runtime serves one stream at
+ * a time. */
+typedef struct iian_pa_runtime iian_pa_runtime;
+
+typedef struct {
+    int32_t max_seqs;            /* requests per step */
+    int32_t max_tokens;          /* new tokens per step */
+    int32_t max_blocks_per_seq;  /* block-table row length */
+    int32_t max_total_blocks;    /* sum of the step's requests' block counts */
+    int32_t n_head, n_head_kv, head_dim, head_dim_v;
+    int32_t block_size, num_blocks;
+    int32_t type_k, type_v;      /* pool types (iian_pa_supported must accept them) */
+} iian_pa_runtime_config;
+
+int iian_pa_runtime_create(const iian_pa_runtime_config *cfg, iian_pa_runtime **out);
+
+/* Waits for every copy and kernel of the device, then frees the runtime (NULL is allowed). */
+void iian_pa_runtime_destroy(iian_pa_runtime *rt);
+
+/* Once per engine step, with the scheduler's state of each scheduled request
+ * s in batch order (host memory): block_ids[s][0 .. n_blocks[s]) its
+ * KVRequestState::block_ids (include/iian/kv_cache.h:93-97), num_computed[s]
+ * and n_new[s] its computed and new token counts.  Copies them through pinned
+ * memory to the device on `stream` (asynchronously; the caller's arrays may be
+ * reused on return) and builds the step's arrays there (iian_pa_build_batch).
+ * Returns IIAN_PA_ERR_ARG when a request's blocks do not cover its context or
+ * a maximum is exceeded. */
+int iian_pa_runtime_begin_step(iian_pa_runtime *rt, void *stream, const int32_t *const *block_ids,
+                               const int32_t *n_blocks, const int32_t *num_computed, const int32_t *n_new,
+                               int32_t n_seqs);
+
+/* Once per layer of the step: the layer's K/V write into k_pool / v_pool at
+ * the step's slots, with RoPE of K and q fused in when rope is non-NULL
+ * (iian_pa_rope_kv_write, q rotated into q_rot, which may equal q) or without
+ * it (iian_pa_kv_write_kv), then paged attention of q (or q_rot) over the
+ * pools into out (iian_pa_attention).  Arrays as those entry points take them. */
+int iian_pa_runtime_layer(iian_pa_runtime *rt, void *stream, const float *q, float *q_rot, const float *k_rows,
+                          const float *v_rows, const iian_pa_rope_params *rope, void *k_pool, void *v_pool,
+                          float scale, float softcap, int32_t causal, int32_t n_swa, float *out);
+
+/* Reads (synchronising `stream`) and clears the runtime's accumulated
+ * error word: the bits of iian_pa_build_batch, iian_pa_kv_write and
+ * iian_pa_attention. */
+int iian_pa_runtime_errors(iian_pa_runtime *rt, void *stream, int32_t *host_err);
 
 /* Dequantises n_rows Q8_0 rows of row_elems values each (pool rows
  * rows_idx[i]) to f32, bit-exactly as ggml's dequantize_row_q8_0

@@ -203,3 +203,28 @@ def test_noalloc_rejects_a_call_beyond_its_scratch(lib):
              0.1, 0.0, 1, 0, 0x8000, None) == _lib.ERR_NULL
     assert f(None, 0x1000, 0x2000, 0x3000, 1, 1, 64, 0x4000, 4, 0x5000, 0x6000, 0x7000, 4, 2, 2, 8, 2, 130, 130, 16,
              0.1, 0.0, 1, 0, 0x8000, None) == _lib.ERR_UNSUPPORTED
+
+
+def test_runtime_rejects_invalid_configs(lib):
+    """iian_pa_runtime_create validates its configuration before allocating
+    anything (no device work on these paths)."""
+    from iian_amd import _lib
+    ok = dict(max_seqs=8, max_tokens=64, max_blocks_per_seq=32, max_total_blocks=256, n_head=32, n_head_kv=8,
+              head_dim=128, head_dim_v=128, block_size=16, num_blocks=1024, type_k=1, type_v=1)
+
+    def create(**over):
+        cfg = _lib.RuntimeConfig(**dict(ok, **over))
+        h = C.c_void_p()
+        st = lib.iian_pa_runtime_create(C.byref(cfg), C.byref(h))
+        assert not h.value
+        return st
+    assert create(max_seqs=0) == _lib.ERR_ARG
+    assert create(n_head=30) == _lib.ERR_ARG            # not a multiple of n_head_kv
+    assert create(block_size=0) == _lib.ERR_ARG
+    assert create(head_dim=130) == _lib.ERR_UNSUPPORTED
+    assert create(type_k=2) == _lib.ERR_UNSUPPORTED
+    assert lib.iian_pa_runtime_create(None, None) == _lib.ERR_NULL
+    lib.iian_pa_runtime_destroy(None)
+    assert lib.iian_pa_runtime_begin_step(None, None, None, None, None, None, 1) == _lib.ERR_NULL
+    assert lib.iian_pa_runtime_layer(None, None, None, None, None, None, None, None, None, 1.0, 0.0, 1, 0,
+                                     None) == _lib.ERR_NULL

@@ -20,7 +20,7 @@ import pytest
 from iian_amd import build as B
 
 # every device source of the library (pa_abi.hip is host code only)
-KERNEL_SOURCES = [s for s in B.SOURCES if s != "pa_abi.hip"]
+KERNEL_SOURCES = [s for s in B.SOURCES if s not in ("pa_abi.hip", "pa_runtime.hip")]   # host code only
 NO_MFMA = {"pa_kv_write.hip", "pa_general.hip", "pa_batch.hip", "pa_rope.hip"}
 PACKED_F32 = re.compile(r"^\s*v_pk_(add|mul|fma)_f32\b", re.M)
 NEG_MIX = re.compile(r"^\s*v_(fma|mad)_mix\w*\s[^\n]*,\s*-", re.M)
