@@ -423,7 +423,7 @@ def config_parity(pa, oracle, name, n_items=None, seed=None):
 
 
 @pytest.mark.parametrize("name,n_items", [
-    ("cfg1", None), ("cfg2", None), ("cfg3", 4096), ("cfg3_p0", 4096), ("cfg4", 2048),
+    ("cfg1", None), ("cfg2", None), ("cfg3", 4096), ("cfg3_prefill", 4096), ("cfg3_p0", 4096), ("cfg4", 2048),
     ("cfg5_global_decode", None), ("cfg5_local_decode", None),
     ("cfg5_global_prefill", 1024), ("cfg5_local_prefill", 1024),
 ])
