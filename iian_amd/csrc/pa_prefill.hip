@@ -34,13 +34,6 @@
 //
 // Workgroups of one (kv head, sequence) share their K/V and are placed on one
 // XCD (its L2) by remapping the linear workgroup id.
-//
-// KV split (f16 prefill launches, KS = 2): a workgroup is two halves of NW
-// waves over the same rows; each half streams its own half of the row
-// block's tiles through its own tile buffers, and half 1 hands its (O, m, l)
-// to half 0 through LDS at the end.  Eight waves at 255 registers fill a CU,
-// so the CU runs one such workgroup at a time, and a ragged row block's chain
-// of tiles is half as long.
 // Semantics: paged_attn_impl (src/iian/paged_attn.cpp:90-146).
 #include "pa_common.h"
 #include "pa_launch.h"
@@ -71,10 +64,9 @@ struct PrefillOcc {
 // tail.  Split decode segments are merged inside the launch (arrive_last):
 // the decode workers finish long before the prefill workgroups, so the merge
 // costs the launch nothing, and the call is one launch.
-template <int D, int NW, int KVT, bool MIXED, int KS>
-__global__ __launch_bounds__(NW * 64 * KS, PrefillOcc<D>::kWavesPerSimd) void pa_prefill_kernel(AttnParams p,
-                                                                                               int n_rb, int n_dec) {
-    static_assert(KS == 1 || (KS == 2 && KVT == 1 && !MIXED), "KV split: f16 prefill launches only");
+template <int D, int NW, int KVT, bool MIXED>
+__global__ __launch_bounds__(NW * 64, PrefillOcc<D>::kWavesPerSimd) void pa_prefill_kernel(AttnParams p, int n_rb,
+                                                                                          int n_dec) {
     int bid = blockIdx.x;
     if constexpr (MIXED) {
         if (bid < n_dec) {
@@ -91,16 +83,18 @@ __global__ __launch_bounds__(NW * 64 * KS, PrefillOcc<D>::kWavesPerSimd) void pa
     constexpr int KK = SH::KK, NO = SH::NO, KSTRIDE = SH::KSTRIDE, VSTRIDE = SH::VSTRIDE;
     constexpr int PT = SH::PT, NH = SH::NH, NS = 16 * NH;   // cells per tile, 32-cell halves, scores per lane
     constexpr bool Q8 = KVT == 8;
-    constexpr int NT = NW * 64;                   // threads of one KV half (the workgroup has KS of them)
+    constexpr int NT = NW * 64;
     constexpr int CPT = SH::CHUNKS / NT;          // f16: 16-byte chunks per thread per tensor
     static_assert(Q8 || CPT * NT == SH::CHUNKS, "tile chunks must divide evenly");
     constexpr int NB = D / 32;                    // Q8_0 blocks per head slice
     constexpr int ITEMS = 2 * PT * NB;        // Q8_0: (tensor, cell, block) staging items
     constexpr int IPT = (ITEMS + NT - 1) / NT;    // Q8_0 items per thread
     constexpr int ROWS = NW * 32;
-    // double-buffered K/V tiles of each KV half: [half][buffer][K tile | V tile]
-    constexpr int TILEB = SH::KBYTES + SH::VBYTES;
-    __shared__ __attribute__((aligned(16))) char lds_tiles[KS * 2 * TILEB];
+    // double-buffered K/V tiles
+    __shared__ __attribute__((aligned(16))) char lds_k0[SH::KBYTES];
+    __shared__ __attribute__((aligned(16))) char lds_k1[SH::KBYTES];
+    __shared__ __attribute__((aligned(16))) char lds_v0[SH::VBYTES];
+    __shared__ __attribute__((aligned(16))) char lds_v1[SH::VBYTES];
     __shared__ __attribute__((aligned(16))) float ksc[2][Q8 ? NB : 1][PT];   // Q8_0 K scales [block][cell]
 
     // XCD-aware mapping: workgroups are dispatched round-robin over the 8 XCDs
@@ -108,24 +102,14 @@ __global__ __launch_bounds__(NW * 64 * KS, PrefillOcc<D>::kWavesPerSimd) void pa
     // all row blocks of a pair run on its XCD, so they share K/V through that
     // XCD's L2, while neighbouring pairs (the ones that carry work when only a
     // few sequences of a batch are prefill chunks) land on different XCDs.
-    // With a KV split the row blocks of a pair are dealt last first: under the
-    // causal mask they carry the most tiles, and a workgroup per CU is
-    // resident, so the longest ones start first.
     const int slot = bid >> 3;
     const int pair = (bid & 7) + 8 * (slot / n_rb);
-    const int rb = KS > 1 ? n_rb - 1 - slot % n_rb : slot % n_rb;
+    const int rb = slot % n_rb;
     if (pair >= p.S * p.Hkv) return;
     const int s = pair / p.Hkv;
     const int hk = pair % p.Hkv;
 
-    // KV half hf of the workgroup: NW waves (wave index wv within the half)
-    // over the same rows as the other half, on its own share of the tiles
-    const int lane = threadIdx.x & 63, hh = lane >> 5, n = lane & 31;
-    const int wave_wg = __builtin_amdgcn_readfirstlane((int) threadIdx.x >> 6);   // wave in the workgroup
-    const int hf = KS > 1 ? wave_wg / NW : 0;
-    const int wave = wave_wg - hf * NW, tid = (int) threadIdx.x - hf * NT;
-    char *const lds_k0 = lds_tiles + (2 * hf) * TILEB, *const lds_v0 = lds_k0 + SH::KBYTES;
-    char *const lds_k1 = lds_tiles + (2 * hf + 1) * TILEB, *const lds_v1 = lds_k1 + SH::KBYTES;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hh = lane >> 5, n = lane & 31;
     const int L = p.seq_lens[s];
     const int q0 = min(max(p.qsl[s], 0), p.T);
     const int nq = min(max(p.qsl[s + 1], q0), p.T) - q0;
@@ -161,11 +145,6 @@ __global__ __launch_bounds__(NW * 64 * KS, PrefillOcc<D>::kWavesPerSimd) void pa
             w_min = min(w_min, __shfl_xor(w_min, o));
             w_max = max(w_max, __shfl_xor(w_max, o));
         }
-        // equal in every lane after the butterflies: scalars from here on
-        wg_min = __builtin_amdgcn_readfirstlane(wg_min);
-        wg_max = __builtin_amdgcn_readfirstlane(wg_max);
-        w_min = __builtin_amdgcn_readfirstlane(w_min);
-        w_max = __builtin_amdgcn_readfirstlane(w_max);
     }
     const bool wave_live = Rw < M;
     int c_hi = L;
@@ -201,17 +180,10 @@ __global__ __launch_bounds__(NW * 64 * KS, PrefillOcc<D>::kWavesPerSimd) void pa
 
     const int bs_mask = (1 << p.bs_log2) - 1;
     const int64_t head_off = (int64_t) hk * D * 2;
-    // this half's tiles: the window's nt tiles in KS runs, run h = tiles
-    // [h*n_it, min(nt, (h+1)*n_it)); every half takes n_it loop steps (the
-    // barriers are shared) and computes only its own n_mine tiles
-    const int nt = c_lo < c_hi ? (c_hi - c_lo + PT - 1) / PT : 0;
-    const int n_it = (nt + KS - 1) / KS;
-    const int first = min(nt, hf * n_it), n_mine = min(nt, first + n_it) - first;
-    const int tile_b = c_lo + first * PT;
     // block-table entries of 64 logical blocks, one per lane, handed out with
     // lane shuffles: a tile's loads never wait on a table read
     TableWindow tw;
-    if (n_mine > 0) table_load(p, s, tile_b >> p.bs_log2, L, tw);
+    if (c_lo < c_hi) table_load(p, s, c_lo >> p.bs_log2, L, tw);
     u32x4 kst[(Q8 || DMA) ? 1 : CPT], vst[(Q8 || DMA) ? 1 : CPT];
     // Q8_0 items of this thread: tensor (0 = K), cell and block; its 34 bytes
     // sit 2 bytes into (odd block) or at the start of (even block) an aligned
@@ -483,72 +455,32 @@ __global__ __launch_bounds__(NW * 64 * KS, PrefillOcc<D>::kWavesPerSimd) void pa
         __builtin_amdgcn_s_setprio(0);
     };
 
-    if (n_it > 0) {   // workgroup-uniform: both halves see the same window
+    if (c_lo < c_hi) {
         int buf = 0;
         if constexpr (DMA) {
             // tile t + 64 streams into the other buffer while tile t is computed;
             // one barrier per tile: every wave's loads of tile t have landed and
             // every wave is done with the buffer the next loads overwrite
-            if (n_mine > 0) load_dma(tile_b, lds_k0, lds_v0);
-            for (int it = 0; it < n_it; it++) {
-                const int tile = tile_b + it * PT;
+            load_dma(c_lo, lds_k0, lds_v0);
+            for (int tile = c_lo; tile < c_hi; tile += PT) {
                 __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this wave's loads of tile t
                 __syncthreads();
-                if (it + 1 < n_mine) load_dma(tile + PT, buf ? lds_k0 : lds_k1, buf ? lds_v0 : lds_v1);
-                if (it < n_mine) compute(tile, buf, buf ? lds_k1 : lds_k0, buf ? lds_v1 : lds_v0);
+                if (tile + PT < c_hi) load_dma(tile + PT, buf ? lds_k0 : lds_k1, buf ? lds_v0 : lds_v1);
+                compute(tile, buf, buf ? lds_k1 : lds_k0, buf ? lds_v1 : lds_v0);
                 buf ^= 1;
             }
         } else {
-            if (n_mine > 0) {
-                load_global(tile_b);
-                store_lds(0);
-            }
+            load_global(c_lo);
+            store_lds(0);
             __syncthreads();
-            for (int it = 0; it < n_it; it++) {
-                const int tile = tile_b + it * PT;
-                const bool has_next = it + 1 < n_mine;
+            for (int tile = c_lo; tile < c_hi; tile += PT) {
+                const bool has_next = tile + PT < c_hi;
                 if (has_next) load_global(tile + PT);
-                if (it < n_mine) compute(tile, buf, buf ? lds_k1 : lds_k0, buf ? lds_v1 : lds_v0);
+                compute(tile, buf, buf ? lds_k1 : lds_k0, buf ? lds_v1 : lds_v0);
                 if (has_next) store_lds(buf ^ 1);
                 __syncthreads();
                 buf ^= 1;
             }
-        }
-    }
-
-    if constexpr (KS == 2) {
-        // Half 1 hands its (O, m, l) to half 0 through LDS (the tile buffers,
-        // free now): element j of wave wv's lane at ((wv * RECF + j) * 64 +
-        // lane) floats.  Half 0 merges them into its registers: with m =
-        // max(m0, m1), O = 2^(m0-m) O0 + 2^(m1-m) O1 and l likewise, per row.
-        constexpr int RECF = NO * 16 + 2;
-        static_assert(NW * 64 * RECF * 4 <= KS * 2 * TILEB, "the hand-over fits the tile buffers");
-        float *const rec = (float *) lds_tiles + wave * RECF * 64 + lane;
-        __syncthreads();   // every wave is done with the tiles
-        if (hf == 1 && wave_live) {
-#pragma unroll
-            for (int m = 0; m < NO; m++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) rec[(m * 16 + r) * 64] = o[m][r];
-            rec[NO * 16 * 64] = m_run;
-            rec[(NO * 16 + 1) * 64] = l_run;
-        }
-        __syncthreads();
-        if (hf == 1 || !wave_live) return;
-        const float m1 = rec[NO * 16 * 64], l1 = rec[(NO * 16 + 1) * 64];
-        const float mn = fmaxf(m_run, m1);
-        float a = 1.f, b = 0.f;
-        if (mn != -INFINITY) {
-            a = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - mn);
-            b = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - mn);
-        }
-        l_run = l_run * a + l1 * b;
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int row = 8 * (r >> 2) + 4 * hh + (r & 3);   // O row of register r
-            const float ar = __shfl(a, row), br = __shfl(b, row);
-#pragma unroll
-            for (int m = 0; m < NO; m++) o[m][r] = o[m][r] * ar + rec[(m * 16 + r) * 64] * br;
         }
     }
 
@@ -569,7 +501,7 @@ __global__ __launch_bounds__(NW * 64 * KS, PrefillOcc<D>::kWavesPerSimd) void pa
     }
 }
 
-template <int D, int NW, int KVT, bool MIXED, int KS = 1>
+template <int D, int NW, int KVT, bool MIXED>
 static hipError_t launch_prefill_t(const AttnParams &p, int max_rows, hipStream_t stream) {
     constexpr int ROWS = NW * 32;
     const int n_rb = (max_rows + ROWS - 1) / ROWS;
@@ -578,16 +510,16 @@ static hipError_t launch_prefill_t(const AttnParams &p, int max_rows, hipStream_
     const int64_t n_dec = MIXED ? ((p.sk_workers + NW - 1) / NW + 7) / 8 * 8 : 0;
     const int64_t nwg = n_dec + n_pf;
     if (nwg > INT32_MAX) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((pa_prefill_kernel<D, NW, KVT, MIXED, KS>), dim3((unsigned) nwg), dim3(NW * 64 * KS), 0, stream,
-                       p, n_rb, (int) n_dec);
+    hipLaunchKernelGGL((pa_prefill_kernel<D, NW, KVT, MIXED>), dim3((unsigned) nwg), dim3(NW * 64), 0, stream, p, n_rb,
+                       (int) n_dec);
     return hipGetLastError();
 }
 
 template <int KVT>
 static hipError_t launch_prefill_kv(const AttnParams &p, int head_dim, int max_rows, hipStream_t stream) {
     switch (head_dim) {
-        case 64: return launch_prefill_t<64, 4, KVT, false, KVT == 1 ? 2 : 1>(p, max_rows, stream);
-        case 128: return launch_prefill_t<128, 4, KVT, false, KVT == 1 ? 2 : 1>(p, max_rows, stream);
+        case 64: return launch_prefill_t<64, 4, KVT, false>(p, max_rows, stream);
+        case 128: return launch_prefill_t<128, 4, KVT, false>(p, max_rows, stream);
         default: return hipErrorInvalidValue;
     }
 }
