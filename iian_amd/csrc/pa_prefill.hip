@@ -145,6 +145,11 @@ __global__ __launch_bounds__(NW * 64, PrefillOcc<D>::kWavesPerSimd) void pa_pref
             w_min = min(w_min, __shfl_xor(w_min, o));
             w_max = max(w_max, __shfl_xor(w_max, o));
         }
+        // equal in every lane after the butterflies: scalars from here on
+        wg_min = __builtin_amdgcn_readfirstlane(wg_min);
+        wg_max = __builtin_amdgcn_readfirstlane(wg_max);
+        w_min = __builtin_amdgcn_readfirstlane(w_min);
+        w_max = __builtin_amdgcn_readfirstlane(w_max);
     }
     const bool wave_live = Rw < M;
     int c_hi = L;
@@ -224,13 +229,41 @@ __global__ __launch_bounds__(NW * 64, PrefillOcc<D>::kWavesPerSimd) void pa_pref
     // DMA tiles: wave instruction q of a tensor fills tile bytes [1024q, 1024q + 1024);
     // lane i's 16 bytes land at 1024q + 16i = row r, chunk slot (16i % 2D)/16,
     // which holds the row's logical chunk slot ^ swz(r)
+    // Rows of a wave instruction: 1024 bytes = RI rows of 2D bytes, rows
+    // RI*q .. RI*q + RI - 1 of the tile, inside one block (RI <= 8 <= block
+    // size, RI*q a multiple of RI).  On a tile that ends inside the sequence
+    // the block id is therefore wave-uniform (a readlane of the table window)
+    // and the lane's part of the address is a per-wave constant.
+    constexpr int RI = 1024 / (2 * D);
+    static_assert(!DMA || (RI <= 8 && (NW * RI) % 16 == 0), "a DMA instruction's rows stay in one block");
+    const int64_t dma_lane_off =
+        (int64_t) (lane / (2 * D / 16)) * p.k_row + head_off +
+        16 * ((lane % (2 * D / 16)) ^ swz((RI * wave + lane / (2 * D / 16)) & 15));
     auto load_dma = [&](int tile, char *Kd, char *Vd) {
         if (((min(tile + PT - 1, L - 1) >> p.bs_log2) - tw.first) >= 64) table_load(p, s, tile >> p.bs_log2, L, tw);
         constexpr int NQ = SH::KBYTES / 1024 / NW;   // instructions per wave per tensor
+        if (tile + PT <= L) {
+#pragma unroll
+            for (int j = 0; j < NQ; j++) {
+                const int r0 = RI * (j * NW + wave);   // first row of this instruction
+                const int blk = __builtin_amdgcn_readlane(tw.id, ((tile + r0) >> p.bs_log2) - tw.first);
+                const uint32_t row = ((uint32_t) blk << p.bs_log2) | (uint32_t) ((tile + r0) & bs_mask);
+                const int64_t off = (int64_t) pool_off(row, p.k_row) + dma_lane_off;
+                const uint32_t lk = __builtin_amdgcn_readfirstlane((uint32_t) (uintptr_t) (Kd + (j * NW + wave) * 1024));
+                const uint32_t lv = __builtin_amdgcn_readfirstlane((uint32_t) (uintptr_t) (Vd + (j * NW + wave) * 1024));
+                lds_load16(p.k_pool + off, lk);
+                lds_load16(p.v_pool + off, lv);
+            }
+            return;
+        }
+        // the sequence's last tile: rows past L-1 repeat cell L-1 (per lane;
+        // the lane index passes through opaque() so that none of this is
+        // held in registers across the tile loop)
+        const int ln = (int) opaque((uint32_t) lane);
 #pragma unroll
         for (int j = 0; j < NQ; j++) {
             const int q = j * NW + wave;
-            const int b = q * 1024 + 16 * lane;
+            const int b = q * 1024 + 16 * ln;
             const int r = b / (2 * D), slot = (b % (2 * D)) >> 4;
             const int c = min(tile + r, L - 1);
             const int32_t blk = __shfl(tw.id, (c >> p.bs_log2) - tw.first);
