@@ -171,11 +171,19 @@ def main() -> int:
 
     cur = [0]   # the replica the next step uses
 
+    # The step's two library calls, each checked once and bound to its
+    # buffers (one ctypes call per issue, as a C++ engine holding its
+    # arguments calls the C ABI), for every copy of the batch cycled through.
+    k_rows, v_rows = w.k_new.contiguous(), w.v_new.contiguous()   # held for the bound calls' lifetime
+    kv_calls = [pa.bind_set_rows_kv(w.k_pool, w.v_pool, k_rows, v_rows, b.slots) for b in batches]
+    attn_calls = [pa.bind_paged_attn(w.q, w.k_pool, w.v_pool, sp.Hkv, w.params, b, out=out, workspace=ws)
+                  for b in batches]
+
     def kv_write():
-        pa.set_rows_kv(w.k_pool, w.v_pool, w.k_new, w.v_new, batches[cur[0]].slots)
+        kv_calls[cur[0]]()
 
     def attention():
-        pa.build_paged_attn(w.q, w.k_pool, w.v_pool, sp.Hkv, w.params, batches[cur[0]], out=out, workspace=ws)
+        attn_calls[cur[0]]()
 
     def step():
         kv_write()

@@ -15,6 +15,8 @@ from .paged_attn import (  # noqa: F401
     PagedBatch,
     RequestBlocks,
     RopeParams,
+    bind_paged_attn,
+    bind_set_rows_kv,
     build_batch,
     build_paged_attn,
     dequant_q8_0,

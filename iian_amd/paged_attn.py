@@ -22,7 +22,7 @@ from __future__ import annotations
 
 import ctypes as C
 from dataclasses import dataclass
-from typing import Optional, Sequence
+from typing import Callable, Optional, Sequence
 
 import numpy as np
 import torch
@@ -330,10 +330,10 @@ def set_rows(pool: KVPool, rows: torch.Tensor, slots: torch.Tensor, err_flag: Op
     return pool
 
 
-def set_rows_kv(k_pool: KVPool, v_pool: KVPool, k_rows: torch.Tensor, v_rows: torch.Tensor, slots: torch.Tensor,
-                err_flag: Optional[torch.Tensor] = None) -> None:
-    """The layer's two set_rows calls (K pool, then V pool, same slots;
-    src/iian/graph.cpp:319-320) as one launch when the pool types match."""
+def _set_rows_kv_args(k_pool: KVPool, v_pool: KVPool, k_rows: torch.Tensor, v_rows: torch.Tensor,
+                      slots: torch.Tensor, err_flag: Optional[torch.Tensor]):
+    """Checks a call of iian_pa_kv_write_kv and returns its argument tuple
+    (the row tensors must already be contiguous)."""
     for pool, rows in ((k_pool, k_rows), (v_pool, v_rows)):
         if rows.dtype != torch.float32 or rows.dim() != 2 or rows.shape[1] != pool.n_embd:
             raise ValueError("rows must be f32 [n_tokens, n_embd]")
@@ -341,12 +341,33 @@ def set_rows_kv(k_pool: KVPool, v_pool: KVPool, k_rows: torch.Tensor, v_rows: to
         raise ValueError("K and V must have the same token count and cell count")
     if slots.dtype != torch.int64 or slots.shape != (k_rows.shape[0],):
         raise ValueError("slots must be int64 [n_tokens]")
-    k_rows, v_rows = k_rows.contiguous(), v_rows.contiguous()
-    lib = _lib.load()
-    st = lib.iian_pa_kv_write_kv(_stream(), k_rows.data_ptr(), v_rows.data_ptr(), k_rows.shape[0], k_rows.shape[1],
-                                 v_rows.shape[1], slots.data_ptr(), k_pool.data.data_ptr(), v_pool.data.data_ptr(),
-                                 k_pool.n_cells, k_pool.type, v_pool.type, _ptr(err_flag))
-    _lib.check("iian_pa_kv_write_kv", st)
+    if not (k_rows.is_contiguous() and v_rows.is_contiguous()):
+        raise ValueError("rows must be contiguous")
+    return (_stream(), k_rows.data_ptr(), v_rows.data_ptr(), k_rows.shape[0], k_rows.shape[1], v_rows.shape[1],
+            slots.data_ptr(), k_pool.data.data_ptr(), v_pool.data.data_ptr(), k_pool.n_cells, k_pool.type,
+            v_pool.type, _ptr(err_flag))
+
+
+def set_rows_kv(k_pool: KVPool, v_pool: KVPool, k_rows: torch.Tensor, v_rows: torch.Tensor, slots: torch.Tensor,
+                err_flag: Optional[torch.Tensor] = None) -> None:
+    """The layer's two set_rows calls (K pool, then V pool, same slots;
+    src/iian/graph.cpp:319-320) as one launch when the pool types match."""
+    args = _set_rows_kv_args(k_pool, v_pool, k_rows.contiguous(), v_rows.contiguous(), slots, err_flag)
+    _lib.check("iian_pa_kv_write_kv", _lib.load().iian_pa_kv_write_kv(*args))
+
+
+def bind_set_rows_kv(k_pool: KVPool, v_pool: KVPool, k_rows: torch.Tensor, v_rows: torch.Tensor,
+                     slots: torch.Tensor, err_flag: Optional[torch.Tensor] = None) -> Callable[[], None]:
+    """set_rows_kv checked once and bound to these buffers and the current
+    stream (contiguous rows), as bind_paged_attn."""
+    args = _set_rows_kv_args(k_pool, v_pool, k_rows, v_rows, slots, err_flag)
+    fn = _lib.load().iian_pa_kv_write_kv
+
+    def call() -> None:
+        st = fn(*args)
+        if st:
+            _lib.check("iian_pa_kv_write_kv", st)
+    return call
 
 
 @dataclass
@@ -440,13 +461,10 @@ def _check_batch(batch: PagedBatch, device: torch.device) -> None:
         raise ValueError("batch.block_tables must have one row per sequence")
 
 
-def build_paged_attn(q: torch.Tensor, k_cache: KVPool, v_cache: KVPool, n_head_kv: int,
-                     params: PagedAttnParams, batch: PagedBatch, out: Optional[torch.Tensor] = None,
-                     workspace: Optional[torch.Tensor] = None,
-                     err_flag: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Paged attention of q [T, H, D] over the pools (paged_attn.cpp:90-169);
-    returns f32 [T, H, Dv].  A workspace from new_workspace() may be passed in
-    and reused across calls."""
+def _attn_call(q: torch.Tensor, k_cache: KVPool, v_cache: KVPool, n_head_kv: int, params: PagedAttnParams,
+               batch: PagedBatch, out: Optional[torch.Tensor], workspace: Optional[torch.Tensor],
+               err_flag: Optional[torch.Tensor]):
+    """Checks a call of iian_pa_attention and returns (out, its argument tuple)."""
     if q.dtype != torch.float32 or q.dim() != 3:
         raise ValueError("q must be f32 [n_tokens, n_head, head_dim]")   # paged_attn.cpp:161
     if not q.is_contiguous():
@@ -481,16 +499,42 @@ def build_paged_attn(q: torch.Tensor, k_cache: KVPool, v_cache: KVPool, n_head_k
         workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
     elif workspace.numel() < need:
         raise ValueError(f"workspace holds {workspace.numel()} bytes, {need} needed")
-    lib = _lib.load()
-    st = lib.iian_pa_attention(_stream(), q.data_ptr(), k_cache.data.data_ptr(), v_cache.data.data_ptr(),
-                               k_cache.type, v_cache.type, num_blocks, batch.block_tables.data_ptr(), max_blocks,
-                               batch.seq_lens.data_ptr(), batch.query_start_loc.data_ptr(), batch.pos.data_ptr(),
-                               T, batch.n_seqs, batch.max_query_len, H, n_head_kv, D, Dv, batch.block_size,
-                               float(params.scale), float(params.softcap), int(bool(params.causal)),
-                               int(params.n_swa), out.data_ptr(), workspace.data_ptr(), workspace.numel(),
-                               _ptr(err_flag))
-    _lib.check("iian_pa_attention", st)
+    args = (_stream(), q.data_ptr(), k_cache.data.data_ptr(), v_cache.data.data_ptr(), k_cache.type, v_cache.type,
+            num_blocks, batch.block_tables.data_ptr(), max_blocks, batch.seq_lens.data_ptr(),
+            batch.query_start_loc.data_ptr(), batch.pos.data_ptr(), T, batch.n_seqs, batch.max_query_len, H,
+            n_head_kv, D, Dv, batch.block_size, float(params.scale), float(params.softcap),
+            int(bool(params.causal)), int(params.n_swa), out.data_ptr(), workspace.data_ptr(), workspace.numel(),
+            _ptr(err_flag))
+    return out, args
+
+
+def build_paged_attn(q: torch.Tensor, k_cache: KVPool, v_cache: KVPool, n_head_kv: int,
+                     params: PagedAttnParams, batch: PagedBatch, out: Optional[torch.Tensor] = None,
+                     workspace: Optional[torch.Tensor] = None,
+                     err_flag: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Paged attention of q [T, H, D] over the pools (paged_attn.cpp:90-169);
+    returns f32 [T, H, Dv].  A workspace from new_workspace() may be passed in
+    and reused across calls."""
+    out, args = _attn_call(q, k_cache, v_cache, n_head_kv, params, batch, out, workspace, err_flag)
+    _lib.check("iian_pa_attention", _lib.load().iian_pa_attention(*args))
     return out
+
+
+def bind_paged_attn(q: torch.Tensor, k_cache: KVPool, v_cache: KVPool, n_head_kv: int, params: PagedAttnParams,
+                    batch: PagedBatch, out: torch.Tensor, workspace: torch.Tensor,
+                    err_flag: Optional[torch.Tensor] = None) -> Callable[[], None]:
+    """The call build_paged_attn would make, checked once and bound to these
+    buffers and the current stream: the returned function issues it again
+    with one ctypes call, as a C caller holding its arguments would.  The
+    buffers must outlive it."""
+    _, args = _attn_call(q, k_cache, v_cache, n_head_kv, params, batch, out, workspace, err_flag)
+    fn = _lib.load().iian_pa_attention
+
+    def call() -> None:
+        st = fn(*args)
+        if st:
+            _lib.check("iian_pa_attention", st)
+    return call
 
 
 def dequant_q8_0(pool: KVPool, rows_idx: torch.Tensor) -> torch.Tensor:

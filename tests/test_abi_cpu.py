@@ -187,6 +187,25 @@ def test_host_wrappers_validate_before_launch():
                          PagedAttnParams(), b)
 
 
+def test_bound_calls_check_their_arguments_when_bound():
+    """bind_paged_attn / bind_set_rows_kv run the same checks as the plain
+    wrappers, once, before anything is bound."""
+    from iian_amd import KVPool, PagedAttnParams, PagedBatch, bind_paged_attn, bind_set_rows_kv
+    pool = KVPool.wrap(torch.zeros((64, 512), dtype=torch.uint8), 256, 1)
+    b = PagedBatch.from_ubatch([3], [0], [3], [[0, 1, 2, 3]], device="cpu")
+    out = torch.empty((1, 4, 128), dtype=torch.float32)
+    ws = torch.empty(16, dtype=torch.uint8)
+    with pytest.raises(ValueError):   # f16 q
+        bind_paged_attn(torch.zeros((1, 4, 128), dtype=torch.float16), pool, pool, 2, PagedAttnParams(), b, out, ws)
+    with pytest.raises(ValueError):   # q not on a GPU
+        bind_paged_attn(torch.zeros((1, 4, 128), dtype=torch.float32), pool, pool, 2, PagedAttnParams(), b, out, ws)
+    rows = torch.zeros((3, 256), dtype=torch.float32)
+    with pytest.raises(ValueError):   # int32 slots
+        bind_set_rows_kv(pool, pool, rows, rows, torch.zeros(3, dtype=torch.int32))
+    with pytest.raises(ValueError):   # non-contiguous rows
+        bind_set_rows_kv(pool, pool, torch.zeros((256, 3)).t(), rows, torch.zeros(3, dtype=torch.int64))
+
+
 def test_noalloc_rejects_a_call_beyond_its_scratch(lib):
     """iian_pa_attention_noalloc checks its need against the 64 MiB scratch on
     the host and returns IIAN_PA_ERR_SCRATCH before any launch (pointers are

@@ -258,6 +258,24 @@ def test_mixed_batch_on_a_side_stream_of_the_caller(pa, oracle, k_type, H, Hkv, 
         assert row_rel_err(o.cpu().numpy(), oracle_attention(oracle, c)).max() <= TOL
 
 
+def test_bound_call_matches_the_plain_call(pa, oracle):
+    """bind_paged_attn issues the same call: bit-identical output, twice."""
+    banner("bound attention call")
+    rng = np.random.default_rng(77)
+    c = make_case(rng, 32, 8, 128, [900, 40, 3000], [1, 1, 1])
+    k, v, batch = to_device(pa, c)
+    prm = pa.PagedAttnParams(scale=c.scale)
+    q = torch.as_tensor(c.q).cuda()
+    ws = pa.new_workspace(c.T, 3, c.H, c.Hkv, c.D, c.bt.shape[1], c.bs)
+    want = pa.build_paged_attn(q, k, v, c.Hkv, prm, batch, workspace=ws).cpu().numpy()
+    out = torch.full((c.T, c.H, c.D), float("nan"), device="cuda")
+    call = pa.bind_paged_attn(q, k, v, c.Hkv, prm, batch, out, ws)
+    call()
+    call()
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), want)
+
+
 def test_attention_all_masked_rows_are_zero(pa, oracle):
     banner("all-masked rows")
     rng = np.random.default_rng(42)
