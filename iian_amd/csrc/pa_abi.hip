@@ -23,9 +23,9 @@ using namespace iian_pa;
 // decode shape, 1536 waves stream the pool fastest (127.0 us against 127.4 at
 // 1280, 129.2 at 1024, 131.4 at 2048, 131.9 at 1792, 136.4 at 1152), and
 // deeper per-wave prefetch gains nothing, so the pool's access pattern, not
-// the number of loads in flight, sets the rate.  In a mixed launch the decode
-// workers are 4 waves per CU: each of their workgroups takes a prefill
-// workgroup's slot on its CU while it runs.  The Q8_0 kernel's workers are
+// the number of loads in flight, sets the rate.  In a mixed launch each
+// decode workgroup takes a prefill workgroup's slot on its CU while it runs
+// (see kF16MixedDecodeWavesPerCu).  The Q8_0 kernel's workers are
 // groups of Hkv workgroups of NW waves over 8 waves per CU: its LDS staging
 // and conversion want two waves per SIMD (half of that measured 1.7x slower at
 // config 4).  At head size 256 a tile moves twice the bytes and 3 waves per CU
@@ -33,7 +33,12 @@ using namespace iian_pa;
 // us at 4 per CU, 58.0 at 2.5, 60.9 at 2, 61.1 at 8; global layer 808 us
 // against 824 us at 4 per CU).
 constexpr int kF16DecodeWavesPerCu = 6;
-constexpr int kF16MixedDecodeWavesPerCu = 4;
+// In the mixed prefill launch the decode workers' workgroups (4 waves each)
+// are dispatched first; at 2 waves per CU they take half the CUs' second
+// workgroup slot instead of every CU's (Qwen3-8B chunked prefill + 32 decode
+// rows: 176.6 against 181.3 us; with one chunk of no prior context 164.5
+// against 162.2 us; 1 per CU 205.6 us, 3 per CU 185.8 us).
+constexpr int kF16MixedDecodeWavesPerCu = 2;
 constexpr int kF16DecodeWavesPerCuD256 = 3;
 constexpr int kQ8DecodeWavesPerCu = 8;
 constexpr int kMaxWavesPerCu = kQ8DecodeWavesPerCu;
