@@ -53,6 +53,7 @@ struct AttnParams {
     int32_t max_q;              // the caller's max_query_len (a sequence with more tokens sets err bit 2)
     int32_t sk_workers;         // stream-K workers: waves (one kv head each) or groups of Hkv workgroups
     int32_t rec_heads;          // kv heads per partial record: 1, or Hkv for grouped workers
+    int32_t seg_waves;          // > 0: f16 decode by pa_decode_seg_kernel, seg_waves waves per segment
 };
 
 __device__ __forceinline__ float wave_max(float v) {

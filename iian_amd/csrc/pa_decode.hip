@@ -135,6 +135,102 @@ hipError_t launch_merge(const AttnParams &p, int head_dim, hipStream_t stream) {
     return hipGetLastError();
 }
 
+// Small decode calls (pa_abi.hip picks it when no sliding window is set and
+// every segment has at most 2*NW tiles): one workgroup of NW waves per
+// (sequence, kv head) segment, wave w attending the segment's tiles
+// [w*per, (w+1)*per), per = ceil(nt/NW) <= 2.  The waves' records stay in LDS
+// and the workgroup merges them after one barrier, so the call is one launch.
+// Its critical path is a chain of dependent memory round trips, so the
+// kernel starts with one round trip for the sequence's length and query
+// range and, beside them, the block-table entries from the wave's earliest
+// possible first tile (cell 32w) on.  Positions are not waited for: the
+// window is taken as [0, L) and every tile is masked by its rows' positions
+// (the tiles past a causal window contribute nothing).  The stream-K kernel
+// spreads such a call's few tiles over 1536 waves and then needs the merge
+// launch and its round trips: at Qwen2.5-0.5B shapes its call takes 15.9 us
+// (decode 8.1 + merge 5.4 us of kernel time) against 15.1 us here, 15.5
+// against 12.8 us with the pool resident in the caches.
+template <int D, int NW>
+__global__ __launch_bounds__(64 * NW) void pa_decode_seg_kernel(AttnParams p) {
+    __shared__ __attribute__((aligned(16))) float lrec[NW][16 * D + 32];
+    const int s = blockIdx.x / p.Hkv, hk = blockIdx.x - s * p.Hkv;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    // one round trip: length, query range, table entries from block
+    // (32 wave) >> bs_log2 on (clamped into the row; entries past the
+    // sequence's blocks are never used)
+    TableWindow tw;
+    tw.first = (wave * kTile) >> p.bs_log2;
+    const int32_t id = p.bt[(int64_t) s * p.max_blocks + min(tw.first + lane, p.max_blocks - 1)];
+    SeqWindow w;
+    w.L = max(p.seq_lens[s], 0);
+    w.q0 = min(max(p.qsl[s], 0), p.T);
+    w.nq = min(max(p.qsl[s + 1], w.q0), p.T) - w.q0;
+    // a sequence with more query tokens than the caller's max_query_len may
+    // have rows this launch does not cover (bit 2, as for_each_piece flags it)
+    if (hk == 0 && threadIdx.x == 0 && w.nq > p.max_q && p.err) atomicOr(p.err, 4);
+    if (w.nq <= 0 || w.nq * p.gqa > 16) return;   // workgroup-uniform
+    w.pmin = -1;        // no tile is taken as unmasked
+    w.pmax = w.L - 1;   // (positions of padding rows, which are never written)
+    w.c_lo = 0;
+    w.c_hi = w.L;
+    w.nt = max(1, (w.L + kTile - 1) / kTile);
+    // as phys_block: a block past the table or a stale id is flagged, never
+    // dereferenced
+    const int nblk = (w.L + (1 << p.bs_log2) - 1) >> p.bs_log2;
+    tw.id = id;
+    if (tw.first + lane < nblk) {
+        if (tw.first + lane >= p.max_blocks || (uint32_t) id >= (uint32_t) p.num_blocks) {
+            if (p.err) atomicOr(p.err, 2);
+            if ((uint32_t) id >= (uint32_t) p.num_blocks) tw.id = 0;
+        }
+    } else {
+        tw.id = 0;
+    }
+    const int per = (w.nt + NW - 1) / NW;
+    Piece pc;
+    pc.s = s;
+    pc.hk = hk;
+    pc.t0 = wave * per;
+    pc.t1 = min(w.nt, pc.t0 + per);
+    pc.seg = s * p.Hkv + hk;
+    pc.rec = pc.rec0 = 0;
+    pc.pieces = (w.nt + per - 1) / per;
+    if (pc.t0 < pc.t1) {
+        // the loaded window holds blocks first .. first+63; small block sizes
+        // can leave the piece's first tile past it
+        const int c1 = min(pc.t0 * kTile + kTile - 1, w.L - 1);
+        if ((c1 >> p.bs_log2) - tw.first >= 64) table_load(p, s, (pc.t0 * kTile) >> p.bs_log2, w.L, tw);
+        decode_piece<D, 1, false, true>(p, w, pc, &lrec[wave][0], &tw);
+    }
+    if (pc.pieces == 1) return;   // the one piece wrote the output
+    __syncthreads();
+    // log-sum-exp merge of the pieces' records, four dims per thread
+    const int M = w.nq * p.gqa;
+    for (int idx = threadIdx.x; idx < M * (D / 4); idx += 64 * NW) {
+        const int r = idx / (D / 4), d = 4 * (idx % (D / 4));
+        float mx = -INFINITY;
+        for (int j = 0; j < pc.pieces; j++) mx = fmaxf(mx, lrec[j][16 * D + 2 * r]);
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        float lsum = 0.f;
+        if (mx != -INFINITY) {
+            for (int j = 0; j < pc.pieces; j++) {
+                const float wgt = __builtin_amdgcn_exp2f(lrec[j][16 * D + 2 * r] - mx);   // 0 for an empty piece
+                lsum += wgt * lrec[j][16 * D + 2 * r + 1];
+                const float4 v = *(const float4 *) &lrec[j][r * D + d];
+                acc.x += wgt * v.x;
+                acc.y += wgt * v.y;
+                acc.z += wgt * v.z;
+                acc.w += wgt * v.w;
+            }
+        }
+        const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+        const int t = w.q0 + r / p.gqa, h = hk * p.gqa + r % p.gqa;
+        *(float4 *) (p.out + ((int64_t) t * p.H + h) * D + d) =
+            make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+    }
+}
+
 template <int D, int NRT>
 static hipError_t launch_decode_t(const AttnParams &p, hipStream_t stream) {
     hipLaunchKernelGGL((pa_decode_f16_kernel<D, NRT>), dim3(p.sk_workers), dim3(64), 0, stream, p);
@@ -146,6 +242,18 @@ hipError_t launch_decode(const AttnParams &p, int head_dim, int kv_type, hipStre
     if (kv_type == 8) return launch_decode_q8(p, head_dim, stream);
     if (kv_type != 1) return hipErrorInvalidValue;
     const int nrt = p.decode_rows > 16 ? 2 : 1;
+    if (p.seg_waves > 0) {
+        if (nrt != 1) return hipErrorInvalidValue;
+        const dim3 grid((unsigned) ((int64_t) p.S * p.Hkv));
+        if (head_dim == 64 && p.seg_waves == kSegWavesD64)
+            hipLaunchKernelGGL((pa_decode_seg_kernel<64, kSegWavesD64>), grid, dim3(64 * kSegWavesD64), 0, stream, p);
+        else if (head_dim == 128 && p.seg_waves == kSegWavesD128)
+            hipLaunchKernelGGL((pa_decode_seg_kernel<128, kSegWavesD128>), grid, dim3(64 * kSegWavesD128), 0, stream,
+                               p);
+        else
+            return hipErrorInvalidValue;
+        return hipGetLastError();
+    }
     switch (head_dim) {
         case 64: return nrt == 1 ? launch_decode_t<64, 1>(p, stream) : launch_decode_t<64, 2>(p, stream);
         case 128: return nrt == 1 ? launch_decode_t<128, 1>(p, stream) : launch_decode_t<128, 2>(p, stream);

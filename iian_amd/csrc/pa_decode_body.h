@@ -82,9 +82,14 @@ __device__ __forceinline__ void load_v(const AttnParams &p, const TableWindow &t
 
 // One piece: window tiles [pc.t0, pc.t1) of sequence pc.s at kv head pc.hk.
 // FUSED: a split segment is merged by its last piece to finish (arrive_last),
-// not by pa_merge_kernel.
-template <int D, int NRT, bool FUSED = false>
-__device__ __forceinline__ void decode_piece(const AttnParams &p, const SeqWindow &w, const Piece &pc) {
+// not by pa_merge_kernel.  LREC (NRT = 1, pa_decode_seg_kernel): the block-
+// table window comes loaded (*tw_pre, covering the piece's first tile), and the
+// piece's record goes to the wave's LDS record lrec (O rows at lrec[r*D + d],
+// (m, l) of row r at lrec[16*D + 2r]) for a merge inside the workgroup.
+template <int D, int NRT, bool FUSED = false, bool LREC = false>
+__device__ __forceinline__ void decode_piece(const AttnParams &p, const SeqWindow &w, const Piece &pc,
+                                             float *lrec = nullptr, const TableWindow *tw_pre = nullptr) {
+    static_assert(!LREC || (NRT == 1 && !FUSED), "LDS records hold one 16-row tile");
     constexpr int KS = D / 32;
     constexpr int DPL = D / 16;
     const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
@@ -94,7 +99,8 @@ __device__ __forceinline__ void decode_piece(const AttnParams &p, const SeqWindo
     const int ce = min(w.c_hi, w.c_lo + pc.t1 * kTile);
 
     TableWindow tw;
-    if (cb < ce) table_load(p, s, cb >> p.bs_log2, w.L, tw);
+    if constexpr (LREC) tw = *tw_pre;
+    else if (cb < ce) table_load(p, s, cb >> p.bs_log2, w.L, tw);
 
     // Q^T B operands (pre-scaled f16 hi/lo pairs), row positions, running state
     f16x8 qh[NRT][KS], ql[NRT][KS];
@@ -224,7 +230,7 @@ __device__ __forceinline__ void decode_piece(const AttnParams &p, const SeqWindo
         }
     }
 
-    if (!FUSED && pc.t0 == 0 && lane == 0) p.seg_info[pc.seg] = make_int2(pc.rec, pc.pieces);
+    if (!FUSED && !LREC && pc.t0 == 0 && lane == 0) p.seg_info[pc.seg] = make_int2(pc.rec, pc.pieces);
 #pragma unroll
     for (int rt = 0; rt < NRT; rt++) {
         float l = l_run[rt];
@@ -250,7 +256,7 @@ __device__ __forceinline__ void decode_piece(const AttnParams &p, const SeqWindo
             for (int i = 0; i < 4; i++) {
                 const int r = rt * 16 + 4 * g + i;
                 if (r < M) {
-                    float *op = rec_o(p, pc.rec, 0, r, D) + DPL * n;
+                    float *op = LREC ? lrec + r * D + DPL * n : rec_o(p, pc.rec, 0, r, D) + DPL * n;
                     if constexpr (FUSED) {
 #pragma unroll
                         for (int m = 0; m < DPL; m += 2) store_pair_agent(op + m, o[rt][m][i], o[rt][m + 1][i]);
@@ -266,6 +272,8 @@ __device__ __forceinline__ void decode_piece(const AttnParams &p, const SeqWindo
             if (g == 0 && r < M) {
                 if constexpr (FUSED)
                     store_pair_agent(rec_ml(p, pc.rec, 0, r), m_run[rt], l);
+                else if constexpr (LREC)
+                    *(float2 *) (lrec + 16 * D + 2 * r) = make_float2(m_run[rt], l);
                 else
                     *(float2 *) rec_ml(p, pc.rec, 0, r) = make_float2(m_run[rt], l);
             }

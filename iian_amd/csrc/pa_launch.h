@@ -29,6 +29,11 @@ struct GenParams {
     int32_t causal, n_swa;
 };
 
+// Waves per segment workgroup of the small-call f16 decode kernel
+// (pa_decode_seg_kernel, p.seg_waves), by head size.
+constexpr int kSegWavesD64 = 16;
+constexpr int kSegWavesD128 = 8;
+
 // Decode / spec-verify kernel (sequences with n_q*gqa <= p.decode_rows) plus the stream-K merge.
 hipError_t launch_decode(const AttnParams &p, int head_dim, int kv_type, hipStream_t stream);
 // The Q8_0-pool variant of launch_decode (pa_decode_q8.hip).

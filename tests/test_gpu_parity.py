@@ -206,6 +206,45 @@ def test_attention_small_cases(pa, oracle, name):
     assert e.max() <= TOL, (name, e.max())
 
 
+SEGMENT_CASES = {
+    # f16 decode calls small enough for the segment-workgroup kernel (every
+    # segment within 2 tiles per wave: 32 tiles at D = 64, 16 at D = 128)
+    "seg_d64": (14, 2, 64, [64, 200, 1000, 17, 1], [1, 1, 1, 1, 1], {}),
+    "seg_d128": (32, 8, 128, [500, 77, 300, 33, 1, 480], [1, 1, 1, 1, 1, 1], {}),
+    # query positions well before the end: the kernel attends [0, L) and the
+    # causal masks remove the tiles past each row's position
+    "seg_d64_random_pos": (8, 2, 64, [900, 640, 100], [2, 1, 2], {"pos_mode": "random"}),
+    "seg_d128_spec2": (16, 4, 128, [480, 33, 200], [2, 2, 1], {}),                   # 8 rows per kv head
+    "seg_d64_softcap": (8, 2, 64, [640, 33], [1, 1], {"softcap": 20.0}),
+    "seg_d128_bs32": (16, 4, 128, [511, 64, 129], [1, 1, 1], {"bs": 32}),
+    "seg_d64_bs8": (8, 2, 64, [1000, 300], [1, 1], {"bs": 8}),   # pieces past the first table window
+}
+
+
+@pytest.mark.parametrize("name", sorted(SEGMENT_CASES))
+def test_segment_decode_matches_stream_k(pa, oracle, name):
+    """Small decode calls run the segment-workgroup kernel (one launch, an LDS
+    merge) when the block table bounds every segment's tiles; padding the
+    table with unused columns makes the same call take the stream-K kernel and
+    its merge launch.  Both against the oracle, and against each other."""
+    H, Hkv, D, lens, nq, kw = SEGMENT_CASES[name]
+    banner(f"segment decode {name} H={H} Hkv={Hkv} D={D} lens={lens} {kw}")
+    c = make_case(np.random.default_rng(zlib.crc32(name.encode())), H, Hkv, D, lens, nq, **kw)
+    want = oracle_attention(oracle, c)
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    seg = gpu_attention(pa, c, err)
+    assert int(err.item()) == 0
+    pad_cols = (4096 + c.bs - 1) // c.bs - c.bt.shape[1]
+    c.bt = np.concatenate([c.bt, np.full((c.bt.shape[0], pad_cols), -1, np.int32)], axis=1)
+    sk = gpu_attention(pa, c, err)
+    assert int(err.item()) == 0
+    e_seg, e_sk = row_rel_err(seg, want), row_rel_err(sk, want)
+    print(f"[gpu] {name}: segment kernel {e_seg.max():.3e}, stream-K {e_sk.max():.3e}", flush=True)
+    assert np.isfinite(seg).all() and np.isfinite(sk).all()
+    assert e_seg.max() <= TOL and e_sk.max() <= TOL, (name, e_seg.max(), e_sk.max())
+    assert row_rel_err(seg, sk).max() <= TOL
+
+
 @pytest.mark.parametrize("k_type,nq", [(F16, 1), (F16, 5), (F16, 64), (Q8_0, 1), (Q8_0, 5), (Q8_0, 64)])
 def test_attention_growing_scores(pa, oracle, k_type, nq):
     """K rows scaled by a ramp 1 .. 16 along each sequence, so every row's
