@@ -311,10 +311,13 @@ int iian_pa_runtime_errors(iian_pa_runtime *rt, void *stream, int32_t *host_err)
  * These are the values the reference's dequantised path computes with.  The
  * MFMA attention kernels enter K as exactly these values (int8 q in f16, the
  * block scale d applied in fp32 after the product), but V as f16(q*d): q*d
- * rounded once to f16, as P is.  A V value beyond the f16 range (|q*d| >
- * 65504, possible only when a block scale exceeds 65504/127 ~ 516) becomes
- * +-inf there, where the reference's fp32 value stays finite.  The general
- * kernel enters both K and V as exactly these values. */
+ * rounded once to f16, as P is (pinned through attention outputs by
+ * test_q8_attention_stages_v_as_f16_of_q_times_d).  A V value beyond the f16
+ * range (|q*d| > 65504, possible only when a block scale exceeds 65504/127 ~
+ * 516) becomes +-inf there, and the outputs it reaches are not finite (inf,
+ * or NaN where a masked cell's zero weight meets it), where the reference's
+ * fp32 value stays finite.  The general kernel enters both K and V as
+ * exactly these values. */
 int iian_pa_dequant_q8_0(void *stream, const void *pool, int64_t n_cells, const int64_t *rows_idx,
                          int64_t n_rows, int64_t row_elems, float *out);
 

@@ -206,6 +206,55 @@ def test_attention_small_cases(pa, oracle, name):
     assert e.max() <= TOL, (name, e.max())
 
 
+def staged_q8_v(v_row_bytes: np.ndarray, n_elems: int) -> np.ndarray:
+    """f16(q*d) of every element of Q8_0 rows, as f32: q (int8) times the
+    block's f16 scale d is exact in f32 and rounded once to f16."""
+    blocks = v_row_bytes.reshape(v_row_bytes.shape[0], n_elems // 32, 34)
+    d = blocks[:, :, :2].copy().view(np.float16).astype(np.float32)          # [rows, blocks, 1]
+    q = blocks[:, :, 2:].copy().view(np.int8).astype(np.float32)             # [rows, blocks, 32]
+    with np.errstate(over="ignore"):
+        return (q * d).astype(np.float16).astype(np.float32).reshape(v_row_bytes.shape[0], n_elems)
+
+
+@pytest.mark.parametrize("kind", ["decode", "prefill"])
+def test_q8_attention_stages_v_as_f16_of_q_times_d(pa, oracle, kind):
+    """Pins the V values the Q8_0 attention kernels compute with: a query row
+    that sees exactly one cell has softmax weight 1 on it, so its output is
+    that cell's V as staged, exactly: f16(q*d) (K enters exactly).  The V
+    rows span block scales from 1e-6 to ~400.  Element 0 of every row sits in
+    a block of scale 600, where 127*d is past the f16 range: those outputs are
+    not finite (the staged value is +-inf, and the tile's masked cells, weight
+    0, turn it into NaN), the documented limit of this staging."""
+    banner(f"q8 staged V values, {kind}")
+    rng = np.random.default_rng(77 if kind == "decode" else 78)
+    H, Hkv, D = 32, 8, 128
+    lens, nq = ([1] * 48, [1] * 48) if kind == "decode" else ([160], [160])
+    c = make_case(rng, H, Hkv, D, lens, nq, k_type=Q8_0, quantize=oracle.quantize_q8_0)
+    n_cells = c.v_pool.shape[0]
+    x = rng.standard_normal((n_cells, Hkv * D)).astype(np.float32)
+    scale = 10.0 ** rng.uniform(-6, 2.6, (n_cells, Hkv * D // 32, 1)).astype(np.float32)
+    x = (x.reshape(n_cells, -1, 32) * scale).reshape(n_cells, -1)
+    x[:, 0] = 127.0 * 600.0
+    c.v_pool = oracle.quantize_q8_0(x)
+    got = gpu_attention(pa, c)
+    staged = staged_q8_v(c.v_pool, Hkv * D)
+    gqa = H // Hkv
+    finite = np.ones((H, D), dtype=bool)
+    finite[:gqa, 0] = False   # element 0 of kv head 0
+    # each checked query row sees one cell: cell 0 of its sequence
+    for t in (range(c.T) if kind == "decode" else [0]):
+        cell = int(c.bt[int(c.seq_idx[t]), 0]) * c.bs
+        want = staged[cell].reshape(Hkv, D)[np.arange(H) // gqa]
+        # exact equality as floats: the weighted sum over the tile's cells
+        # cannot keep the sign of a zero (-0 + 0 = +0), every other bit must match
+        bad = np.flatnonzero(got[t][finite] != want[finite])
+        if len(bad):
+            print(f"[gpu] row {t}: {len(bad)} differ; got {got[t][finite][bad[:8]]} want {want[finite][bad[:8]]}",
+                  flush=True)
+        assert len(bad) == 0, t
+        assert not np.isfinite(got[t][~finite]).any(), t
+
+
 SEGMENT_CASES = {
     # f16 decode calls small enough for the segment-workgroup kernel (every
     # segment within 2 tiles per wave: 32 tiles at D = 64, 16 at D = 128)
