@@ -429,15 +429,19 @@ def test_split_merge_with_garbage_workspace(pa, oracle, k_type, nqs):
     assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
 
 
-@pytest.mark.parametrize("k_type,nqs", SPLIT_CASES)
-def test_graph_replays_match_eager(pa, oracle, k_type, nqs):
+GRAPH_LENS = [5000, 700, 3000, 2500]
+
+
+@pytest.mark.parametrize("k_type,nqs,lens", [(k, n, GRAPH_LENS) for k, n in SPLIT_CASES] +
+                         [(F16, (1, 1, 1, 1), [500, 300, 77, 200])])   # the segment-workgroup kernel
+def test_graph_replays_match_eager(pa, oracle, k_type, nqs, lens):
     """A call captured in a graph and replayed four times, with eager calls
     of another batch on the same workspace in between, gives the eager call's
     bits on every replay (a replay reuses its call's merge-counter tag; the
     merging piece resets each counter it completes)."""
-    banner(f"graph replays k_type={k_type} nq={nqs}")
+    banner(f"graph replays k_type={k_type} nq={nqs} lens={lens}")
     rng = np.random.default_rng(49 + sum(nqs))
-    c = make_case(rng, 32, 8, 128, [5000, 700, 3000, 2500], list(nqs), k_type=k_type, quantize=oracle.quantize_q8_0)
+    c = make_case(rng, 32, 8, 128, lens, list(nqs), k_type=k_type, quantize=oracle.quantize_q8_0)
     k, v, batch = to_device(pa, c)
     prm = pa.PagedAttnParams(scale=c.scale)
     q = torch.as_tensor(c.q).cuda()
