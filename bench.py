@@ -56,9 +56,9 @@ def pmc_traffic(config: str):
     return None if rec is None else int(rec["traffic_bytes_per_launch"])
 
 
-def launch_kernels(sp, pa, max_blocks: int, block_size: int) -> str:
+def launch_kernels(sp, pa, max_blocks: int, block_size: int, cus: int) -> str:
     """The kernels one iian_pa_attention call of this workload launches (as
-    run_attention in pa_abi.hip picks them)."""
+    run_attention in pa_abi.hip picks them on a device of `cus` CUs)."""
     gqa = sp.H // sp.Hkv
     rows = [int(n) * gqa for n in sp.n_q]
     has_dec = any(0 < r <= 32 for r in rows)
@@ -73,10 +73,16 @@ def launch_kernels(sp, pa, max_blocks: int, block_size: int) -> str:
         if has_pf and d <= 128:   # the mixed-batch instantiation, also without decode rows
             extra = " (decode pieces in the same grid, merged there)" if has_dec else ""
             return f"pa_prefill_kernel<{d}, f16, mixed>{extra}"
-        # small decode-only calls: one workgroup per (sequence, kv head)
-        seg_waves = {64: 16, 128: 8}.get(d, 0)
+        # decode-only calls with short or window-bounded segments: one
+        # workgroup per (sequence, kv head)
+        seg_waves = {64: 16, 128: 8, 256: 4}.get(d, 0)
         tiles = (max_blocks * block_size + 31) // 32
-        if not has_pf and max(rows) <= 16 and sp.n_swa <= 0 and seg_waves and tiles <= 2 * seg_waves:
+        if sp.n_swa > 0:
+            wtiles = min(tiles, (sp.n_swa + max(sp.n_q) - 1 + 62) // 32)
+            seg = wtiles <= 16 * seg_waves and len(sp.n_q) * sp.Hkv >= cus
+        else:
+            seg = tiles <= 2 * seg_waves
+        if not has_pf and max(rows) <= 16 and seg_waves and seg:
             return f"pa_decode_seg_kernel<{d}, {seg_waves}>"
     if has_dec and has_pf:
         return f"{pf} || {dec} (two streams)"
@@ -299,8 +305,9 @@ def main() -> int:
         "attn_tok_per_s": round(w.T / (attn_ms * 1e-3), 1),
         "roofline": {
             "bound": "mfma" if mfma_bound else "hbm",
-            "kernel": "iian_pa_attention (" + launch_kernels(sp, pa, int(w.batch.block_tables.shape[1]),
-                                                             w.batch.block_size) + ")",
+            "kernel": "iian_pa_attention (" + launch_kernels(
+                sp, pa, int(w.batch.block_tables.shape[1]), w.batch.block_size,
+                torch.cuda.get_device_properties(torch.cuda.current_device()).multi_processor_count) + ")",
             "achieved": round(attn_tfs if mfma_bound else attn_gbs, 1),
             "peak": MFMA_F16_PEAK_TFLOPS if mfma_bound else HBM_PEAK_GBS,
             "unit": "TFLOP/s" if mfma_bound else "GB/s",

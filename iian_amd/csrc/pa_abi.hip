@@ -442,15 +442,23 @@ int run_attention(hipStream_t st, const float *q, const void *k_pool, const void
     }
     p.rec_stride = (int64_t) p.rec_heads * p.decode_rows * head_dim_v + kRecordPad;
     const bool decode_only = max_rows <= p.decode_rows;
-    // Small f16 decode calls: with no sliding window, when the block-table
+    // f16 decode calls with short or window-bounded segments: one workgroup
+    // per (sequence, kv head) attends and merges in LDS, in one launch
+    // (pa_decode_seg_kernel).  With no sliding window, when the block-table
     // width leaves no segment more than two tiles per wave of a segment
-    // workgroup, one workgroup per (sequence, kv head) attends and merges in
-    // LDS, in one launch (pa_decode_seg_kernel).
-    if (decode_only && type_k == IIAN_PA_TYPE_F16 && p.decode_rows == 16 && n_swa <= 0 &&
-        (head_dim == 64 || head_dim == 128)) {
-        const int sw = head_dim == 64 ? kSegWavesD64 : kSegWavesD128;
-        const int64_t cells = (int64_t) max_blocks << bs_log2;
-        if ((cells + kTile - 1) / kTile <= 2 * sw) p.seg_waves = sw;
+    // workgroup; with one, when a decode step's window (n_swa cells plus the
+    // query span, tile-aligned) keeps every wave within kSegSwaTilesPerWave
+    // tiles and the call has a segment for every CU.
+    if (decode_only && type_k == IIAN_PA_TYPE_F16 && p.decode_rows == 16 &&
+        (head_dim == 64 || head_dim == 128 || head_dim == 256)) {
+        const int sw = head_dim == 64 ? kSegWavesD64 : head_dim == 128 ? kSegWavesD128 : kSegWavesD256;
+        const int64_t tiles = (((int64_t) max_blocks << bs_log2) + kTile - 1) / kTile;
+        if (n_swa <= 0) {
+            if (tiles <= 2 * sw) p.seg_waves = sw;
+        } else {
+            const int64_t wtiles = std::min<int64_t>(tiles, ((int64_t) n_swa + max_query_len - 1 + 2 * kTile - 2) / kTile);
+            if (wtiles <= (int64_t) kSegSwaTilesPerWave * sw && (int64_t) n_seqs * n_head_kv >= cus) p.seg_waves = sw;
+        }
     }
     // Mixed batch over an f16 pool (head size 64 or 128): one launch holds the
     // prefill workgroups and, after them, the decode rows' stream-K workers,

@@ -135,33 +135,45 @@ hipError_t launch_merge(const AttnParams &p, int head_dim, hipStream_t stream) {
     return hipGetLastError();
 }
 
-// Small decode calls (pa_abi.hip picks it when no sliding window is set and
-// every segment has at most 2*NW tiles): one workgroup of NW waves per
-// (sequence, kv head) segment, wave w attending the segment's tiles
-// [w*per, (w+1)*per), per = ceil(nt/NW) <= 2.  The waves' records stay in LDS
-// and the workgroup merges them after one barrier, so the call is one launch.
-// Its critical path is a chain of dependent memory round trips, so the
-// kernel starts with one round trip for the sequence's length and query
-// range and, beside them, the block-table entries from the wave's earliest
-// possible first tile (cell 32w) on.  Positions are not waited for: the
-// window is taken as [0, L) and every tile is masked by its rows' positions
-// (the tiles past a causal window contribute nothing).  The stream-K kernel
-// spreads such a call's few tiles over 1536 waves and then needs the merge
-// launch and its round trips: at Qwen2.5-0.5B shapes its call takes 15.9 us
-// (decode 8.1 + merge 5.4 us of kernel time) against 15.1 us here, 15.5
-// against 12.8 us with the pool resident in the caches.
+// Decode calls whose segments are short, or bounded by a sliding window
+// (pa_abi.hip picks it): one workgroup of NW waves per (sequence, kv head)
+// segment, wave w attending the segment's tiles [w*per, (w+1)*per),
+// per = ceil(nt/NW).  The waves' records stay in LDS and the workgroup merges
+// them after one barrier, so the call is one launch, with no records in HBM
+// and no merge launch.  Its critical path is a chain of dependent memory round
+// trips:
+// - no window: one round trip carries the sequence's length and query range
+//   and, beside them, the block-table entries from the wave's earliest
+//   possible first tile (cell 32w) on.  Positions are not waited for: the
+//   window is taken as [0, L) and every tile is masked by its rows' positions
+//   (the tiles past a causal window contribute nothing).
+// - sliding window: the window starts at the rows' smallest position minus
+//   n_swa - 1, so a second round trip loads the positions and, beside them,
+//   the table entries of the window that positions L - nq .. L - 1 (a decode
+//   step's) would give; when the positions say otherwise the wave reloads its
+//   entries.
+// The stream-K kernel spreads a small call's few tiles over 1536 waves and
+// then needs the merge launch and its round trips: at Qwen2.5-0.5B shapes its
+// call takes 15.9 us (decode 8.1 + merge 5.4 us of kernel time) against 15.1
+// us here, 15.5 against 12.8 us with the pool resident in the caches.  At
+// Gemma3-12B's sliding-window layer (256 segments of 1024-cell windows, D =
+// 256) the call takes 54.4-54.6 us here against 56.8-58.8 us (4 waves per
+// segment; 3 waves measured the same, 2 waves 58.5 us).
 template <int D, int NW>
 __global__ __launch_bounds__(64 * NW) void pa_decode_seg_kernel(AttnParams p) {
     __shared__ __attribute__((aligned(16))) float lrec[NW][16 * D + 32];
     const int s = blockIdx.x / p.Hkv, hk = blockIdx.x - s * p.Hkv;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    // one round trip: length, query range, table entries from block
-    // (32 wave) >> bs_log2 on (clamped into the row; entries past the
-    // sequence's blocks are never used)
+    const bool swa = p.n_swa > 0;
+    // table entries clamped into the row (entries past the sequence's blocks
+    // are never used)
     TableWindow tw;
-    tw.first = (wave * kTile) >> p.bs_log2;
-    const int32_t id = p.bt[(int64_t) s * p.max_blocks + min(tw.first + lane, p.max_blocks - 1)];
+    int32_t id = 0;
+    if (!swa) {
+        tw.first = (wave * kTile) >> p.bs_log2;
+        id = p.bt[(int64_t) s * p.max_blocks + min(tw.first + lane, p.max_blocks - 1)];
+    }
     SeqWindow w;
     w.L = max(p.seq_lens[s], 0);
     w.q0 = min(max(p.qsl[s], 0), p.T);
@@ -170,11 +182,33 @@ __global__ __launch_bounds__(64 * NW) void pa_decode_seg_kernel(AttnParams p) {
     // have rows this launch does not cover (bit 2, as for_each_piece flags it)
     if (hk == 0 && threadIdx.x == 0 && w.nq > p.max_q && p.err) atomicOr(p.err, 4);
     if (w.nq <= 0 || w.nq * p.gqa > 16) return;   // workgroup-uniform
-    w.pmin = -1;        // no tile is taken as unmasked
-    w.pmax = w.L - 1;   // (positions of padding rows, which are never written)
-    w.c_lo = 0;
-    w.c_hi = w.L;
-    w.nt = max(1, (w.L + kTile - 1) / kTile);
+    if (!swa) {
+        w.pmin = -1;        // no tile is taken as unmasked
+        w.pmax = w.L - 1;   // (positions of padding rows, which are never written)
+        w.c_lo = 0;
+        w.c_hi = w.L;
+    } else {
+        const int lo_guess = max(0, w.L - w.nq - p.n_swa + 1) & ~(kTile - 1);
+        const int per_guess = (max(1, (w.L - lo_guess + kTile - 1) / kTile) + NW - 1) / NW;
+        tw.first = (lo_guess + wave * per_guess * kTile) >> p.bs_log2;
+        id = p.bt[(int64_t) s * p.max_blocks + min(tw.first + lane, p.max_blocks - 1)];
+        // the window of the rows' positions, as seq_window forms it
+        int mn = INT32_MAX, mx = INT32_MIN;
+        if (lane < w.nq) mn = mx = p.pos[w.q0 + lane];
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) {
+            mn = min(mn, __shfl_xor(mn, o));
+            mx = max(mx, __shfl_xor(mx, o));
+        }
+        w.pmin = __builtin_amdgcn_readfirstlane(mn);
+        w.pmax = __builtin_amdgcn_readfirstlane(mx);
+        int hi = w.L;
+        if (p.causal) hi = min(hi, max(w.pmax + 1, 0));
+        const int lo = max(0, w.pmin - p.n_swa + 1) & ~(kTile - 1);
+        w.c_lo = lo;
+        w.c_hi = max(hi, lo);
+    }
+    w.nt = max(1, (w.c_hi - w.c_lo + kTile - 1) / kTile);
     // as phys_block: a block past the table or a stale id is flagged, never
     // dereferenced
     const int nblk = (w.L + (1 << p.bs_log2) - 1) >> p.bs_log2;
@@ -197,10 +231,13 @@ __global__ __launch_bounds__(64 * NW) void pa_decode_seg_kernel(AttnParams p) {
     pc.rec = pc.rec0 = 0;
     pc.pieces = (w.nt + per - 1) / per;
     if (pc.t0 < pc.t1) {
-        // the loaded window holds blocks first .. first+63; small block sizes
-        // can leave the piece's first tile past it
-        const int c1 = min(pc.t0 * kTile + kTile - 1, w.L - 1);
-        if ((c1 >> p.bs_log2) - tw.first >= 64) table_load(p, s, (pc.t0 * kTile) >> p.bs_log2, w.L, tw);
+        // the loaded entries cover blocks first .. first+63: small block sizes
+        // can leave the piece's first tile past them, and positions other than
+        // the guessed ones can move it before them
+        const int cb = w.c_lo + pc.t0 * kTile;
+        const int c1 = min(cb + kTile - 1, w.L - 1);
+        if ((cb >> p.bs_log2) < tw.first || (c1 >> p.bs_log2) - tw.first >= 64)
+            table_load(p, s, cb >> p.bs_log2, w.L, tw);
         decode_piece<D, 1, false, true>(p, w, pc, &lrec[wave][0], &tw);
     }
     if (pc.pieces == 1) return;   // the one piece wrote the output
@@ -249,6 +286,9 @@ hipError_t launch_decode(const AttnParams &p, int head_dim, int kv_type, hipStre
             hipLaunchKernelGGL((pa_decode_seg_kernel<64, kSegWavesD64>), grid, dim3(64 * kSegWavesD64), 0, stream, p);
         else if (head_dim == 128 && p.seg_waves == kSegWavesD128)
             hipLaunchKernelGGL((pa_decode_seg_kernel<128, kSegWavesD128>), grid, dim3(64 * kSegWavesD128), 0, stream,
+                               p);
+        else if (head_dim == 256 && p.seg_waves == kSegWavesD256)
+            hipLaunchKernelGGL((pa_decode_seg_kernel<256, kSegWavesD256>), grid, dim3(64 * kSegWavesD256), 0, stream,
                                p);
         else
             return hipErrorInvalidValue;

@@ -29,10 +29,13 @@ struct GenParams {
     int32_t causal, n_swa;
 };
 
-// Waves per segment workgroup of the small-call f16 decode kernel
-// (pa_decode_seg_kernel, p.seg_waves), by head size.
+// Waves per segment workgroup of the f16 segment decode kernel
+// (pa_decode_seg_kernel, p.seg_waves), by head size, and the most tiles per
+// wave a sliding-window call may give it.
 constexpr int kSegWavesD64 = 16;
 constexpr int kSegWavesD128 = 8;
+constexpr int kSegWavesD256 = 4;
+constexpr int kSegSwaTilesPerWave = 16;
 
 // Decode / spec-verify kernel (sequences with n_q*gqa <= p.decode_rows) plus the stream-K merge.
 hipError_t launch_decode(const AttnParams &p, int head_dim, int kv_type, hipStream_t stream);

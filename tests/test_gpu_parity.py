@@ -267,6 +267,8 @@ SEGMENT_CASES = {
     "seg_d64_softcap": (8, 2, 64, [640, 33], [1, 1], {"softcap": 20.0}),
     "seg_d128_bs32": (16, 4, 128, [511, 64, 129], [1, 1, 1], {"bs": 32}),
     "seg_d64_bs8": (8, 2, 64, [1000, 300], [1, 1], {"bs": 8}),   # pieces past the first table window
+    "seg_d256": (16, 8, 256, [200, 77, 256, 1], [1, 1, 1, 1], {}),   # 8 tiles over 4 waves
+    "seg_d256_spec": (16, 8, 256, [250, 40], [4, 8], {}),            # 8 and 16 rows per kv head
 }
 
 
@@ -286,6 +288,51 @@ def test_segment_decode_matches_stream_k(pa, oracle, name):
     pad_cols = (4096 + c.bs - 1) // c.bs - c.bt.shape[1]
     c.bt = np.concatenate([c.bt, np.full((c.bt.shape[0], pad_cols), -1, np.int32)], axis=1)
     sk = gpu_attention(pa, c, err)
+    assert int(err.item()) == 0
+    e_seg, e_sk = row_rel_err(seg, want), row_rel_err(sk, want)
+    print(f"[gpu] {name}: segment kernel {e_seg.max():.3e}, stream-K {e_sk.max():.3e}", flush=True)
+    assert np.isfinite(seg).all() and np.isfinite(sk).all()
+    assert e_seg.max() <= TOL and e_sk.max() <= TOL, (name, e_seg.max(), e_sk.max())
+    assert row_rel_err(seg, sk).max() <= TOL
+
+
+def window_case(name, rng):
+    """Sliding-window decode calls with a segment for every CU of an MI355X
+    (S * Hkv = 256), which run the segment-workgroup kernel."""
+    H, Hkv, D, n_swa, kw = WINDOW_SEGMENT_CASES[name]
+    kw = dict(kw)
+    S = 256 // Hkv
+    lens = rng.integers(40, 3 * n_swa, S)
+    nq = rng.integers(1, 16 // (H // Hkv) + 1, S) if kw.pop("spec", False) else np.ones(S, np.int64)
+    return make_case(rng, H, Hkv, D, lens, nq, n_swa=n_swa, **kw)
+
+
+WINDOW_SEGMENT_CASES = {
+    "swa_d256": (16, 8, 256, 256, {}),
+    # positions far from the end of each sequence: the window the kernel
+    # guesses from the length is wrong, and the waves reload their entries
+    "swa_d256_random_pos": (16, 8, 256, 256, {"pos_mode": "random"}),
+    "swa_d128_spec": (32, 8, 128, 300, {"spec": True}),               # 4 .. 16 rows per kv head
+    "swa_d64_bs8": (16, 8, 64, 500, {"bs": 8}),                       # windows past 64 table entries
+    "swa_d128_softcap": (32, 8, 128, 200, {"softcap": 25.0}),
+}
+
+
+@pytest.mark.parametrize("name", sorted(WINDOW_SEGMENT_CASES))
+def test_segment_window_decode_matches_stream_k(pa, oracle, name):
+    """Sliding-window decode calls whose segments fill the device run the
+    segment-workgroup kernel; a max_query_len that asks for 32-row decode tiles
+    makes the same call take the stream-K kernel and its merge launch.  Both
+    against the oracle, and against each other."""
+    if torch.cuda.get_device_properties(0).multi_processor_count > 256:
+        pytest.skip("the cases give 256 segments: fewer than this device's CUs")
+    banner(f"segment window decode {name} {WINDOW_SEGMENT_CASES[name]}")
+    c = window_case(name, np.random.default_rng(zlib.crc32(name.encode())))
+    want = oracle_attention(oracle, c)
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    seg = gpu_attention(pa, c, err)
+    assert int(err.item()) == 0
+    sk = gpu_attention(pa, c, err, max_query_len=16 // (c.H // c.Hkv) + 1)
     assert int(err.item()) == 0
     e_seg, e_sk = row_rel_err(seg, want), row_rel_err(sk, want)
     print(f"[gpu] {name}: segment kernel {e_seg.max():.3e}, stream-K {e_sk.max():.3e}", flush=True)
