@@ -89,7 +89,10 @@ __global__ __launch_bounds__(NW * 64, (D == 128 && KVT == 1) ? 4 : (D <= 128 ? 2
     const int s = pair / p.Hkv;
     const int hk = pair % p.Hkv;
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, n = lane & 15;
+    // wave index in a scalar register, so that the tile-load rows derived from
+    // it stay in SALU (cfg5 global prefill 4947-5022 against 5015-5085 us)
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, g = lane >> 4,
+              n = lane & 15;
     const int L = p.seq_lens[s];
     const int q0 = min(max(p.qsl[s], 0), p.T);
     const int nq = min(max(p.qsl[s + 1], q0), p.T) - q0;
