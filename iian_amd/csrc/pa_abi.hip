@@ -427,6 +427,7 @@ int run_attention(hipStream_t st, const float *q, const void *k_pool, const void
     p.causal = causal ? 1 : 0;
     p.n_swa = n_swa;
     p.max_q = max_query_len;
+    p.cus_per_xcd = std::max(1, cus / 8);
     // Row budget of the decode kernel: one 16-row MFMA tile, or two when that
     // covers every sequence of the call (spec-verify); larger sequences go to
     // the prefill kernel.

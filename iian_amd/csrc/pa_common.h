@@ -54,6 +54,7 @@ struct AttnParams {
     int32_t sk_workers;         // stream-K workers: waves (one kv head each) or groups of Hkv workgroups
     int32_t rec_heads;          // kv heads per partial record: 1, or Hkv for grouped workers
     int32_t seg_waves;          // > 0: f16 decode by pa_decode_seg_kernel, seg_waves waves per segment
+    int32_t cus_per_xcd;        // CUs per XCD: workgroups b and b + 8*cus_per_xcd of a launch share a CU
 };
 
 __device__ __forceinline__ float wave_max(float v) {

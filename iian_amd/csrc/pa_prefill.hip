@@ -98,13 +98,20 @@ __global__ __launch_bounds__(NW * 64, PrefillOcc<D>::kWavesPerSimd) void pa_pref
     __shared__ __attribute__((aligned(16))) float ksc[2][Q8 ? NB : 1][PT];   // Q8_0 K scales [block][cell]
 
     // XCD-aware mapping: workgroups are dispatched round-robin over the 8 XCDs
-    // (bid % 8).  (sequence, kv head) pairs are dealt round-robin to XCDs and
-    // all row blocks of a pair run on its XCD, so they share K/V through that
-    // XCD's L2, while neighbouring pairs (the ones that carry work when only a
-    // few sequences of a batch are prefill chunks) land on different XCDs.
+    // (bid % 8) and within an XCD round-robin over its CUs, so the XCD's slots
+    // s and s + cus_per_xcd share a CU.  (sequence, kv head) pairs are dealt
+    // round-robin to XCDs and all row blocks of a pair run on its XCD, so they
+    // share K/V through that XCD's L2, while neighbouring pairs (the ones that
+    // carry work when only a few sequences of a batch are prefill chunks) land
+    // on different XCDs.  A pair whose first slot falls in an odd round of
+    // slots takes its row blocks in reverse, so that a pair's heavy late row
+    // blocks (they attend the most cells) share CUs with another pair's light
+    // early ones and get the CU to themselves sooner (Qwen3-8B chunked prefill
+    // -1.9%, with decode rows -4.5%).  Per pair, so every row block is taken once.
     const int slot = bid >> 3;
-    const int pair = (bid & 7) + 8 * (slot / n_rb);
-    const int rb = slot % n_rb;
+    const int pair_x = slot / n_rb;
+    const int pair = (bid & 7) + 8 * pair_x;
+    const int rb = (((pair_x * n_rb) / p.cus_per_xcd) & 1) ? n_rb - 1 - slot % n_rb : slot % n_rb;
     if (pair >= p.S * p.Hkv) return;
     const int s = pair / p.Hkv;
     const int hk = pair % p.Hkv;
