@@ -578,11 +578,9 @@ hipError_t launch_mixed_f16(const AttnParams &p, int head_dim, int max_rows, hip
 
 hipError_t launch_prefill(const AttnParams &p, int head_dim, int kv_type, int max_rows, hipStream_t stream) {
     if (head_dim == 256) return launch_prefill16(p, head_dim, kv_type, max_rows, stream);
-    switch (kv_type) {
-        case 1: return launch_prefill_kv<1>(p, head_dim, max_rows, stream);
-        case 8: return launch_prefill_kv<8>(p, head_dim, max_rows, stream);
-        default: return hipErrorInvalidValue;
-    }
+    // f16 pools at head size 64 and 128 take launch_mixed_f16, with or
+    // without decode rows
+    return kv_type == 8 ? launch_prefill_kv<8>(p, head_dim, max_rows, stream) : hipErrorInvalidValue;
 }
 
 }  // namespace iian_pa
