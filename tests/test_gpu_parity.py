@@ -517,6 +517,50 @@ def test_graph_replays_match_eager(pa, oracle, k_type, nqs, lens):
         assert np.array_equal(o2.cpu().numpy(), other), it
 
 
+def test_q8_many_sequences_split_over_workers(pa, oracle):
+    """Q8_0 spec-verify over at least as many sequences as stream-K workers
+    (130 sequences of 5 query tokens: 128 workers of 2-wave workgroups on an
+    MI355X), ragged, so segments split at worker boundaries.  Against the
+    oracle, over workspaces filled with garbage (same bits every time), and
+    through graph replays."""
+    banner("q8 many sequences split over workers")
+    rng = np.random.default_rng(50)
+    c = make_case(rng, 32, 8, 128, rng.integers(60, 700, 130), [5] * 130, k_type=Q8_0,
+                  quantize=oracle.quantize_q8_0)
+    k, v, batch = to_device(pa, c)
+    prm = pa.PagedAttnParams(scale=c.scale)
+    q = torch.as_tensor(c.q).cuda()
+    ws = pa.new_workspace(c.T, 130, c.H, c.Hkv, c.D, c.bt.shape[1], c.bs)
+    outs = []
+    for fill in ("ff", "random", "zero"):
+        if fill == "ff":
+            ws.fill_(255)
+        elif fill == "random":
+            ws.copy_(torch.randint(0, 256, ws.shape, dtype=torch.uint8, generator=torch.Generator().manual_seed(8)))
+        else:
+            ws.zero_()
+        outs.append(pa.build_paged_attn(q, k, v, c.Hkv, prm, batch, workspace=ws).cpu().numpy())
+    e = row_rel_err(outs[0], oracle_attention(oracle, c))
+    print(f"[gpu] q8 many sequences: max row rel err {e.max():.3e}", flush=True)
+    assert e.max() <= TOL
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+    out = torch.empty_like(q)
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        pa.build_paged_attn(q, k, v, c.Hkv, prm, batch, out=out, workspace=ws)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        pa.build_paged_attn(q, k, v, c.Hkv, prm, batch, out=out, workspace=ws)
+    for it in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy(), outs[0]), it
+
+
 def test_attention_bad_block_id_is_clamped_and_flagged(pa):
     banner("bad block id")
     rng = np.random.default_rng(43)
