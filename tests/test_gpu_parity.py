@@ -165,6 +165,10 @@ SMALL = {
     # blocks), and the smallest block size
     "swa_prefill_d128_bs64": (8, 2, 128, [2000, 1200], [256, 100], {"n_swa": 480, "bs": 64}),
     "prefill_d128_bs8": (8, 2, 128, [700, 300], [200, 64], {"bs": 8}),
+    # 12 row blocks per (sequence, kv head) and 4 pairs per XCD: the fourth
+    # pair's slots start in the second round of CU slots, so it takes its row
+    # blocks in reverse (a round that 12 does not divide)
+    "prefill_nrb12_reversed": (32, 8, 128, [600, 500, 450, 700], [384, 384, 384, 384], {}),
     "random_positions": (8, 2, 64, [300, 200], [6, 40], {"pos_mode": "random"}),
     # Q8_0 pools (decode / spec-verify kernel)
     "q8_decode_gqa4_d128": (32, 8, 128, [513, 77, 2048, 33], [1, 1, 1, 1], {"k_type": Q8_0}),
