@@ -8,7 +8,10 @@ paged GQA decode attention over the block pool, inputs resident in HBM.
 ``value`` is the achieved algorithmic HBM bandwidth of the whole step (GB/s);
 ``attn_tok_per_s`` the query tokens per second of one layer-call.
 ``roofline`` is measured live for the dominant launch (the attention call) with
-HIP events on the stream it runs on; ``cpu_baseline`` times the CPU oracle
+HIP events on the stream it runs on: one pair around K back-to-back calls
+(``avg_launch_us``), and one pair around each call of K steps
+(``avg_launch_us_evented``, which adds the event records' own cost to short
+calls); ``cpu_baseline`` times the CPU oracle
 (a restatement of the reference's paged_attn_impl) on this host.
 """
 from __future__ import annotations
@@ -225,7 +228,12 @@ def main() -> int:
     ms_step = wall * 1e3 / args.steps
     log(f"timed {args.steps} steps: {ms_step * 1e3:.1f} us/step")
 
-    # dominant launch: the attention call alone, HIP events on its stream
+    # dominant launch: the attention call alone, HIP events on its stream.
+    # First a pair around each call of K steps (the KV write between calls),
+    # then one pair around K back-to-back calls.  The second is the launch's
+    # average duration: an event record between kernels costs about 2.7 us of
+    # its own at most configurations, and the back-to-back average agrees with
+    # the kernel trace's (rocprofv3) where the per-call pairs exceed it.
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
     for a, b in ev:
         kv_write()
@@ -234,10 +242,19 @@ def main() -> int:
         b.record(stream)
         cur[0] = (cur[0] + 1) % len(batches)
     torch.cuda.synchronize()
-    attn_ms = sum(a.elapsed_time(b) for a, b in ev) / len(ev)
+    attn_ev_ms = sum(a.elapsed_time(b) for a, b in ev) / len(ev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(args.steps):
+        attention()
+        cur[0] = (cur[0] + 1) % len(batches)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    attn_ms = e0.elapsed_time(e1) / args.steps
     attn_gbs = b_attn / (attn_ms * 1e-3) / 1e9
     attn_tfs = flops / (attn_ms * 1e-3) / 1e12
-    log(f"attention: {attn_ms * 1e3:.1f} us/launch, {attn_gbs:.0f} GB/s algorithmic, {attn_tfs:.1f} TFLOP/s")
+    log(f"attention: {attn_ms * 1e3:.1f} us/launch back to back ({attn_ev_ms * 1e3:.1f} us between per-call "
+        f"events), {attn_gbs:.0f} GB/s algorithmic, {attn_tfs:.1f} TFLOP/s")
 
     # per-step work beside the layer-call, each timed alone with HIP events:
     # the device-side batch build (once per step, iian_pa_build_batch) and the
@@ -316,6 +333,7 @@ def main() -> int:
             "algorithmic_bytes_per_launch": b_attn,
             "flops_per_launch": flops,
             "avg_launch_us": round(attn_ms * 1e3, 2),
+            "avg_launch_us_evented": round(attn_ev_ms * 1e3, 2),
         },
     }
     if not args.no_cpu_baseline:
