@@ -377,14 +377,17 @@ int run_attention(hipStream_t st, const float *q, const void *k_pool, const void
         // Split each row block's KV range until the launch holds about 8
         // workgroups per CU, keeping at least 2 tiles per range of the
         // longest sequence the tables can hold, and the records inside the
-        // workspace: [T*H][n_split] rows of (Dv floats) + (m, l).
+        // workspace: [T*H][n_split] rows of (Dv floats) + (m, l).  The
+        // no-allocation entry point's workspace is the scratch array, so its
+        // records must also fit kScratchBytes (one range needs none).
         const int64_t base = (int64_t) n_seqs * n_head_kv * g.n_rb;
         const int64_t max_tiles = ((int64_t) max_blocks * block_size + g.tile_cells - 1) / g.tile_cells;
         int64_t ns = (8LL * cus + base - 1) / base;
         ns = std::min<int64_t>(ns, std::max<int64_t>(1, max_tiles / 2));
         ns = std::min<int64_t>(ns, 64);
         const size_t per_split = (size_t) n_tokens * n_head * (size_t) (head_dim_v + 2) * sizeof(float) + 512;
-        ns = std::min<int64_t>(ns, (int64_t) (wl.total / per_split));
+        const size_t rec_cap = src.scratch ? std::min(wl.total, kScratchBytes) : wl.total;
+        ns = std::min<int64_t>(ns, (int64_t) (rec_cap / per_split));
         g.n_split = (int) std::max<int64_t>(ns, 1);
         const size_t o_bytes = align256((size_t) n_tokens * n_head * g.n_split * head_dim_v * sizeof(float));
         const size_t need = g.n_split > 1 ? o_bytes + (size_t) n_tokens * n_head * g.n_split * 2 * sizeof(float) : 0;

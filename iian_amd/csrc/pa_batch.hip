@@ -72,6 +72,14 @@ __global__ __launch_bounds__(256) void pa_build_batch_kernel(BatchParams p) {
         p.pos[t] = ps;
         p.slots[t] = slot;
     }
+    // Tokens past the last request's (the counts sum to less than n_tokens,
+    // flagged above): slot -1, so a KV write of n_tokens rows skips them
+    // instead of writing to whatever the buffers held.
+    if (s == p.S - 1)
+        for (int t = q0 + max(nn, 0) + tid; t < p.T; t += 256) {
+            p.pos[t] = 0;
+            p.slots[t] = -1;
+        }
 }
 
 // Sliding-window block freeing (the reference's planned "free out-of-window

@@ -277,20 +277,42 @@ class PagedAttnRuntime:
         nb = np.array([a.size for a in arrs], np.int32)
         nc = np.ascontiguousarray(num_computed, dtype=np.int32)
         nn = np.ascontiguousarray(n_new, dtype=np.int32)
+        self._T = None
         st = self._lib.iian_pa_runtime_begin_step(self._h, _stream(), ptrs, nb.ctypes.data, nc.ctypes.data,
                                                   nn.ctypes.data, S)
         _lib.check("iian_pa_runtime_begin_step", st)
+        self._T = int(nn.sum())
 
     def layer(self, q: torch.Tensor, k_rows: torch.Tensor, v_rows: torch.Tensor, k_pool: KVPool, v_pool: KVPool,
               params: PagedAttnParams, out: torch.Tensor, rope: Optional[RopeParams] = None,
               q_rot: Optional[torch.Tensor] = None) -> None:
-        for t in (q, k_rows, v_rows, out):
-            if t.dtype != torch.float32 or not t.is_contiguous() or not t.is_cuda:
-                raise ValueError("q, k_rows, v_rows and out must be contiguous f32 GPU tensors")
+        c = self.cfg
+        T = getattr(self, "_T", None)
+        if T is None:
+            raise ValueError("layer() needs a successful begin_step() first")
+        dev = q.device
+        shapes = ((q, (T, c.n_head, c.head_dim)), (k_rows, (T, c.n_head_kv * c.head_dim)),
+                  (v_rows, (T, c.n_head_kv * c.head_dim_v)), (out, (T, c.n_head, c.head_dim_v)))
+        for t, shp in shapes:
+            if tuple(t.shape) != shp:
+                raise ValueError(f"expected a tensor of shape {shp} for this step, got {tuple(t.shape)}")
+        for t, _ in shapes:
+            if t.dtype != torch.float32 or not t.is_contiguous() or not t.is_cuda or t.device != dev:
+                raise ValueError("q, k_rows, v_rows and out must be contiguous f32 tensors on one GPU")
+        n_cells = c.num_blocks * c.block_size
+        for pool, ty, e in ((k_pool, c.type_k, c.n_head_kv * c.head_dim), (v_pool, c.type_v, c.n_head_kv * c.head_dim_v)):
+            if pool.type != ty or pool.n_cells != n_cells or pool.n_embd != e or pool.data.device != dev:
+                raise ValueError(f"pools must hold {n_cells} cells of {e} elements of the configured types on q's device")
         prm = None
         if rope is not None:
             if q_rot is None:
                 raise ValueError("rope needs q_rot (q itself for an in-place rotation)")
+            if (q_rot.dtype != torch.float32 or not q_rot.is_contiguous() or q_rot.device != dev
+                    or q_rot.shape != q.shape):
+                raise ValueError("q_rot must be a contiguous f32 tensor shaped like q on q's device")
+            ff = rope.freq_factors
+            if ff is not None and (ff.dtype != torch.float32 or ff.numel() < rope.n_dims // 2 or ff.device != dev):
+                raise ValueError("freq_factors must be f32 with n_dims/2 values on q's device")
             prm = _lib.RopeParams(rope.n_dims, rope.mode, rope.n_ctx_orig, rope.freq_base, rope.freq_scale,
                                   rope.ext_factor, rope.attn_factor, rope.beta_fast, rope.beta_slow,
                                   _ptr(rope.freq_factors))
@@ -405,19 +427,28 @@ def rope_set_rows_kv(k_pool: KVPool, v_pool: KVPool, k_rows: torch.Tensor, v_row
         raise ValueError("pool rows must hold n_head_kv heads")
     if slots.dtype != torch.int64 or slots.shape != (T,) or pos.dtype != torch.int32 or pos.shape != (T,):
         raise ValueError("slots must be int64 [T] and pos int32 [T]")
+    dev = k_rows.device
+    if not (slots.is_contiguous() and pos.is_contiguous()) or slots.device != dev or pos.device != dev:
+        raise ValueError("slots and pos must be contiguous and on the rows' device")
+    if v_rows.device != dev or k_pool.data.device != dev or v_pool.data.device != dev:
+        raise ValueError("rows and pools must be on one device")
     D = k_pool.n_embd // n_head_kv
     H = 0
     if q is not None:
-        if q.dtype != torch.float32 or q.dim() != 3 or q.shape[0] != T or q.shape[2] != D or not q.is_contiguous():
-            raise ValueError("q must be contiguous f32 [T, H, D]")
+        if (q.dtype != torch.float32 or q.dim() != 3 or q.shape[0] != T or q.shape[2] != D or not q.is_contiguous()
+                or q.device != dev):
+            raise ValueError("q must be contiguous f32 [T, H, D] on the rows' device")
         H = q.shape[1]
         if q_out is None:
             q_out = torch.empty_like(q)
-        elif q_out.shape != q.shape or q_out.dtype != q.dtype or not q_out.is_contiguous():
-            raise ValueError("q_out must match q")
+        elif (q_out.shape != q.shape or q_out.dtype != q.dtype or not q_out.is_contiguous()
+              or q_out.device != dev):
+            raise ValueError("q_out must match q (shape, dtype, device) and be contiguous")
+    elif q_out is not None:
+        raise ValueError("q_out without q")
     ff = rope.freq_factors
-    if ff is not None and (ff.dtype != torch.float32 or ff.numel() < rope.n_dims // 2 or not ff.is_cuda):
-        raise ValueError("freq_factors must be f32 with n_dims/2 values on the GPU")
+    if ff is not None and (ff.dtype != torch.float32 or ff.numel() < rope.n_dims // 2 or ff.device != dev):
+        raise ValueError("freq_factors must be f32 with n_dims/2 values on the rows' device")
     prm = _lib.RopeParams(rope.n_dims, rope.mode, rope.n_ctx_orig, rope.freq_base, rope.freq_scale, rope.ext_factor,
                           rope.attn_factor, rope.beta_fast, rope.beta_slow, _ptr(ff))
     k_rows, v_rows = k_rows.contiguous(), v_rows.contiguous()

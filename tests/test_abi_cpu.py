@@ -247,3 +247,31 @@ def test_runtime_rejects_invalid_configs(lib):
     assert lib.iian_pa_runtime_begin_step(None, None, None, None, None, None, 1) == _lib.ERR_NULL
     assert lib.iian_pa_runtime_layer(None, None, None, None, None, None, None, None, None, 1.0, 0.0, 1, 0,
                                      None) == _lib.ERR_NULL
+
+
+def test_runtime_layer_checks_the_step_shapes():
+    """PagedAttnRuntime.layer checks q, the rows, out and the pools against
+    the configuration and the token count of the last begin_step before the
+    C runtime reads rt->T rows (a runtime object without device buffers:
+    nothing may reach the library)."""
+    from iian_amd import _lib
+    from iian_amd.paged_attn import KVPool, PagedAttnParams, PagedAttnRuntime
+    rt = PagedAttnRuntime.__new__(PagedAttnRuntime)
+    rt.cfg = _lib.RuntimeConfig(8, 64, 32, 256, 8, 2, 64, 64, 16, 4, 1, 1)
+    rt._h = C.c_void_p()
+    T = 5
+    q, out = torch.zeros((T, 8, 64)), torch.zeros((T, 8, 64))
+    kr, vr = torch.zeros((T, 128)), torch.zeros((T, 128))
+    pool = KVPool.wrap(torch.zeros((64, 256), dtype=torch.uint8), 128, 1)
+    prm = PagedAttnParams()
+    with pytest.raises(ValueError, match="begin_step"):
+        rt.layer(q, kr, vr, pool, pool, prm, out)
+    rt._T = T
+    for bad in (dict(q=torch.zeros((T + 1, 8, 64))), dict(kr=torch.zeros((T, 64))), dict(vr=torch.zeros((T - 1, 128))),
+                dict(out=torch.zeros((T, 8, 32)))):
+        a = dict(q=q, kr=kr, vr=vr, out=out, **{})
+        a.update(bad)
+        with pytest.raises(ValueError, match="shape"):
+            rt.layer(a["q"], a["kr"], a["vr"], pool, pool, prm, a["out"])
+    with pytest.raises(ValueError, match="GPU"):   # right shapes, host tensors
+        rt.layer(q, kr, vr, pool, pool, prm, out)

@@ -92,3 +92,30 @@ def test_build_batch_flags_inconsistent_requests(pa):
     assert slots[:12].tolist() == [4 * 16 + 4 + i for i in range(12)] and (slots[12:20] == -1).all()
     assert slots[20] == 5 * 16 and slots[21] == 99 * 16
     assert b.query_start_loc.cpu().tolist() == [0, 20, 21, 22]
+
+
+def test_build_batch_fills_tokens_past_the_counts(pa):
+    """n_tokens above the sum of the new-token counts: bit 3 is set, and the
+    tokens past the last request get pos 0 and slot -1, so a KV write of
+    n_tokens rows skips them (bit 0) and leaves the pool untouched."""
+    req = pa.RequestBlocks.pack([[3, 4], [5]], [10, 0], [6, 1])   # 7 new tokens
+    T = 12
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    b = pa.build_batch(req, T, 16, 4, 64, err_flag=err)
+    b.pos.fill_(12345)            # stale contents must be overwritten
+    b.slots.fill_(7)
+    pa.build_batch(req, T, 16, 4, 64, err_flag=err, out=b)
+    torch.cuda.synchronize()
+    assert int(err.item()) & 8
+    assert b.pos.cpu().tolist()[7:] == [0] * 5
+    assert b.slots.cpu().tolist()[7:] == [-1] * 5
+    assert b.slots.cpu().tolist()[:7] == [3 * 16 + 10 + i for i in range(6)] + [5 * 16]
+    pool = pa.KVPool(64 * 16, 64, pa.GGML_TYPE_F16, device="cuda")
+    pool.data.zero_()
+    err2 = torch.zeros(1, dtype=torch.int32, device="cuda")
+    pa.set_rows(pool, torch.ones((T, 64), device="cuda"), b.slots, err2)
+    torch.cuda.synchronize()
+    assert int(err2.item()) & 1
+    rows = pool.data.view(64 * 16, -1).cpu()
+    written = (rows != 0).any(dim=1).nonzero().flatten().tolist()
+    assert written == sorted([3 * 16 + 10 + i for i in range(6)] + [5 * 16])

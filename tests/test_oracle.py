@@ -423,6 +423,36 @@ def test_rope_rows_pairs_and_invariants(oracle, mode):
         assert np.array_equal(back[:, :, :nd], ys[:, :, :nd])
 
 
+@pytest.mark.parametrize("mode", [0, 2])
+def test_rope_rows_rotation_direction(oracle, mode):
+    """Each pair (x0, x1) becomes [[cos t, -sin t], [sin t, cos t]] (x0, x1)
+    with t = pos * base^(-2i/n_dims) (ggml-cpu/ops.cpp:6063-6080), computed
+    here in float64 from the closed form, within the fp32 angle-chain bound
+    of test_rope_cache_closed_form plus the rounding of the two products.  A
+    rotation by -t (a flipped sine) is far outside that bound, which the test
+    checks too, so the direction is pinned independently of the oracle."""
+    rng = np.random.default_rng(21 + mode)
+    T, Hh, D, nd, base = 16, 2, 128, 128, 10000.0
+    x = rng.standard_normal((T, Hh * D)).astype(np.float32)
+    pos = rng.integers(1, 3000, T).astype(np.int32)
+    y = oracle.rope_rows(x, pos, Hh, D, nd, mode=mode, freq_base=base).reshape(T, Hh, D).astype(np.float64)
+    xs = x.reshape(T, Hh, D).astype(np.float64)
+    i = np.arange(nd // 2)
+    e0 = 2 * i if mode == 0 else i
+    e1 = e0 + 1 if mode == 0 else i + nd // 2
+    th = pos[:, None, None].astype(np.float64) * np.power(base, -2.0 * i / nd)[None, None, :]
+    c, s_ = np.cos(th), np.sin(th)
+    x0, x1 = xs[:, :, e0], xs[:, :, e1]
+    want0, want1 = x0 * c - x1 * s_, x0 * s_ + x1 * c
+    ang = th * (2 * i + 2) * 2.0 ** -24 + 2.0 ** -23                 # |cos/sin error| of the fp32 chain
+    bound = (np.abs(x0) + np.abs(x1)) * (ang + 2.0 ** -23) + 2.0 ** -22
+    assert (np.abs(y[:, :, e0] - want0) <= bound).all()
+    assert (np.abs(y[:, :, e1] - want1) <= bound).all()
+    flip0, flip1 = x0 * c + x1 * s_, -x0 * s_ + x1 * c             # rotation by -t
+    miss = (np.abs(y[:, :, e0] - flip0) > bound) | (np.abs(y[:, :, e1] - flip1) > bound)
+    assert miss.mean() > 0.9
+
+
 def test_rope_cos_sin_against_libm(oracle):
     """The oracle's cos/sin are the correctly rounded values of the fp32 angle;
     glibc's cosf/sinf (what ggml calls) agree with them on all but a small

@@ -8,8 +8,10 @@ kernels with the same plan, and the scratch keeps the first call's contents
 when the second starts.  Cases: f16 decode whose segments split over stream-K
 workers (records + merge launch), a mixed f16 batch (in-launch merge through
 tagged counters), a Q8_0 mixed batch (prefill and decode kernels in order on
-the caller's stream instead of a side stream), and the general fp32 path with
-split ranges.
+the caller's stream instead of a side stream), the general fp32 path with
+split ranges, and a head size of 512 on the general path whose split ranges
+are capped by the scratch size (there the two entry points plan different
+range counts, so the outputs agree within fp32 rounding, not bit for bit).
 """
 import ctypes as C
 
@@ -58,6 +60,10 @@ CASES = [
     ("f16_mixed_one_launch", 32, 8, 128, [900, 5000, 700], [200, 1, 1], [600, 3000], [64, 1], {}),
     ("q8_mixed_in_order", 32, 8, 128, [900, 5000, 700], [200, 1, 1], [600, 3000], [64, 1], {"k_type": Q8_0}),
     ("f32_general_splits", 8, 2, 96, [6000, 700], [1, 3], [1500], [1], {"k_type": F32}),
+    # head size 512 on the general path: 64 ranges of records would need 67.4 MB, more than the
+    # scratch holds, so the no-allocation call plans fewer ranges than the workspace call (same
+    # values within fp32 rounding, not the same bits)
+    ("f16_general_d512_scratch_cap", 16, 1, 512, [1500], [32], [1200], [32], {"exact": False}),
 ]
 
 
@@ -67,6 +73,8 @@ def test_noalloc_matches_workspace_entry_on_two_calls(pa, oracle, case):
     print(f"\n[gpu] noalloc {name}", flush=True)
     lib = pa._lib.load()
     rng = np.random.default_rng(61)
+    kw = dict(kw)
+    exact = kw.pop("exact", True)
     for lens, nq in ((lens1, nq1), (lens2, nq2)):
         c = make_case(rng, H, Hkv, D, lens, nq, quantize=oracle.quantize_q8_0, **kw)
         q, k, v, batch = device_case(c)
@@ -78,7 +86,10 @@ def test_noalloc_matches_workspace_entry_on_two_calls(pa, oracle, case):
         torch.cuda.synchronize()
         got = out.cpu().numpy()
         assert int(err.item()) == 0
-        assert np.array_equal(got, want), (name, len(lens), np.abs(got - want).max())
+        if exact:
+            assert np.array_equal(got, want), (name, len(lens), np.abs(got - want).max())
+        else:
+            assert row_rel_err(got, want).max() <= 1e-5, (name, len(lens), np.abs(got - want).max())
         e = row_rel_err(got, oracle.paged_attention(c.q, c.k_pool, c.v_pool, c.k_type, c.v_type, c.bt, c.seq_lens,
                                                     c.seq_idx, c.pos, c.Hkv, c.Dv, c.bs, c.scale, n_threads=16))
         assert e.max() <= 2e-3, (name, e.max())
