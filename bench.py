@@ -42,6 +42,7 @@ WORKLOADS = {
     "cfg5_local_decode": "Gemma3-12B local layer decode (n_swa=1024), H16/Hkv8/D256, 32 seqs",
     "cfg5_global_prefill": "Gemma3-12B global layer, 256-token prefill chunk per seq, 32 seqs",
     "cfg5_local_prefill": "Gemma3-12B local layer (n_swa=1024), 256-token prefill chunk per seq, 32 seqs",
+    "phi3_decode": "Phi-3.5-mini paged decode, H32/Hkv32/D96, 64 seqs, ctx log-uniform [512,8192], f16 KV",
 }
 
 
@@ -64,6 +65,10 @@ def launch_kernels(sp, pa, max_blocks: int, block_size: int, cus: int) -> str:
     run_attention in pa_abi.hip picks them on a device of `cus` CUs)."""
     gqa = sp.H // sp.Hkv
     rows = [int(n) * gqa for n in sp.n_q]
+    if sp.D == 96 and sp.kv_type == pa.GGML_TYPE_F16 and max(rows) <= 32:
+        return "pa_decode_f16_kernel<96> + pa_merge_kernel<96>"
+    if sp.D not in (64, 128, 256):
+        return "pa_general_kernel + pa_general_merge_kernel"
     has_dec = any(0 < r <= 32 for r in rows)
     has_pf = any(r > 32 for r in rows)
     d = sp.D
@@ -277,12 +282,30 @@ def main() -> int:
         torch.cuda.synchronize()
         return t0.elapsed_time(t1) / reps * 1e3
 
-    build_us = timed(lambda: pa.build_batch(req, w.T, sp.block_size, w.block_tables.shape[1], sp.num_blocks,
-                                            out=nb_dev))
-    rope_us = timed(lambda: pa.rope_set_rows_kv(w.k_pool, w.v_pool, w.k_new, w.v_new, w.batch.slots, w.batch.pos,
-                                                rope, sp.Hkv, q=w.q, q_out=q_rot))
+    # bound calls (one ctypes call per issue), as kv_write and attention above
+    build_us = timed(pa.bind_build_batch(req, w.T, sp.block_size, w.block_tables.shape[1], sp.num_blocks, nb_dev))
+    rope_call = pa.bind_rope_set_rows_kv(w.k_pool, w.v_pool, k_rows, v_rows, w.batch.slots, w.batch.pos, rope,
+                                         sp.Hkv, q=w.q, q_out=q_rot)
+    rope_us = timed(rope_call)
     kvw_us = timed(kv_write)
-    log(f"beside the call: build_batch {build_us:.1f} us, rope+kv write {rope_us:.1f} us, kv write {kvw_us:.1f} us")
+    # the unfused sequence the fused launch replaces: RoPE of q and K into f32
+    # rows (the same kernel with an f32 "pool" of T rows at slots 0..T-1; it
+    # also copies V there, 4*T*Hkv*Dv bytes the reference's rope would not
+    # move), then the layer's two set_rows (iian_pa_kv_write_kv)
+    k_tmp = pa.KVPool(w.T, sp.Hkv * sp.D, pa.GGML_TYPE_F32)
+    v_tmp = pa.KVPool(w.T, sp.Hkv * sp.D, pa.GGML_TYPE_F32)
+    ident = torch.arange(w.T, dtype=torch.int64, device="cuda")
+    rope_only = pa.bind_rope_set_rows_kv(k_tmp, v_tmp, k_rows, v_rows, ident, w.batch.pos, rope, sp.Hkv, q=w.q,
+                                         q_out=q_rot)
+    k_rot = k_tmp.data.view(torch.float32).view(w.T, sp.Hkv * sp.D)
+    kv_after = pa.bind_set_rows_kv(w.k_pool, w.v_pool, k_rot, v_rows, w.batch.slots)
+
+    def unfused():
+        rope_only()
+        kv_after()
+    unfused_us = timed(unfused)
+    log(f"beside the call: build_batch {build_us:.1f} us, rope+kv write {rope_us:.1f} us (unfused rope then kv "
+        f"write {unfused_us:.1f} us), kv write {kvw_us:.1f} us")
 
     if args.copy_calibration:
         # a copy kernel that reads and writes exactly n bytes: its FETCH_SIZE /
@@ -317,7 +340,7 @@ def main() -> int:
             "kv_copies_cycled": replicas,
         },
         "beside_the_call_us": {"build_batch": round(build_us, 2), "rope_kv_write": round(rope_us, 2),
-                               "kv_write": round(kvw_us, 2)},
+                               "rope_then_kv_write_unfused": round(unfused_us, 2), "kv_write": round(kvw_us, 2)},
         "hbm_frac_of_peak": round(value / HBM_PEAK_GBS, 4),
         "attn_tok_per_s": round(w.T / (attn_ms * 1e-3), 1),
         "roofline": {
@@ -343,8 +366,9 @@ def main() -> int:
         t_share = max(1, min(avail, CPU_SHARE))
         t_half = max(1, min(nproc // 2, CPU_SHARE))
         log(f"timing the CPU oracle on the same step: {model}, nproc {nproc}, {avail} cores available, "
-            f"{t_share} threads (and 1)")
+            f"{t_share} threads, {t_half} threads and 1")
         med = cpu_baseline(w, t_share)
+        med_half = cpu_baseline(w, t_half) if t_half != t_share else med
         med1 = cpu_baseline(w, 1, runs=3 if med * t_share < 3.0 else 1)
         res["cpu_baseline"] = {
             "value": round(b_step / med / 1e9, 2), "unit": "GB/s", "cores": t_share, "kind": "port",
@@ -353,6 +377,8 @@ def main() -> int:
             "cpu_model": model, "nproc": nproc, "cores_available": avail,
             "threads_policy": f"min(nproc, hardware_concurrency()/2 = {nproc // 2}) capped at the "
                               f"{CPU_SHARE}-core host share of one GPU on this pool: {t_share} and {t_half} threads",
+            "half_concurrency": {"threads": t_half, "value": round(b_step / med_half / 1e9, 2),
+                                 "ms_per_step": round(med_half * 1e3, 1)},
             "single_thread": {"value": round(b_step / med1 / 1e9, 3), "ms_per_step": round(med1 * 1e3, 1)},
         }
     print(json.dumps(res), flush=True)

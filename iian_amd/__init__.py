@@ -15,7 +15,9 @@ from .paged_attn import (  # noqa: F401
     PagedBatch,
     RequestBlocks,
     RopeParams,
+    bind_build_batch,
     bind_paged_attn,
+    bind_rope_set_rows_kv,
     bind_set_rows_kv,
     build_batch,
     build_paged_attn,

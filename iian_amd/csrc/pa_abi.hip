@@ -340,7 +340,12 @@ int run_attention(hipStream_t st, const float *q, const void *k_pool, const void
     const int bs_log2 = log2_exact(block_size);
     const int gqa = n_head / n_head_kv;
 
-    if (!mfma_path(type_k, type_v, head_dim, head_dim_v, bs_log2)) {
+    // f16 pools at head size 96 (Phi-3) take the MFMA decode kernel when every
+    // sequence of the call is a decode or spec-verify row set; batches with
+    // prefill chunks take the general kernel
+    const bool decode96 = type_k == IIAN_PA_TYPE_F16 && type_v == IIAN_PA_TYPE_F16 && head_dim == 96 &&
+                          head_dim_v == 96 && bs_log2 >= 3 && (int64_t) max_query_len * gqa <= kDecodeRowsMax;
+    if (!mfma_path(type_k, type_v, head_dim, head_dim_v, bs_log2) && !decode96) {
         // General fp32 path.  Cell indices within a sequence and pool rows
         // are int32 / int64 there.
         if ((int64_t) max_blocks * block_size > INT32_MAX) return IIAN_PA_ERR_UNSUPPORTED;
@@ -469,7 +474,21 @@ int run_attention(hipStream_t st, const float *q, const void *k_pool, const void
     // which fill the CUs the MFMA-bound prefill leaves, and merge their split
     // segments themselves.
     const bool mixed_one_launch = !decode_only && type_k == IIAN_PA_TYPE_F16 && head_dim <= 128;
+    // No sequence can be a decode row when even the smallest possible query
+    // count, T - (S - 1) * max_query_len (the others holding at most
+    // max_query_len each), is above the decode row budget: then no decode
+    // worker or decode launch is issued at all, and the row budget drops to
+    // 0 so that the prefill kernel covers every sequence.  (A max_query_len
+    // below the batch's largest query count, flagged by bit 2, can break the
+    // bound; a decode sequence is then attended by the prefill kernel, not
+    // left unwritten.)
+    const bool no_decode_rows =
+        !decode_only && ((int64_t) n_tokens - (int64_t) (n_seqs - 1) * max_query_len) * gqa > p.decode_rows;
     if (mixed_one_launch) p.sk_workers = kF16MixedDecodeWavesPerCu * cus;
+    if (no_decode_rows) {
+        p.decode_rows = 0;
+        p.sk_workers = 0;
+    }
     const WorkspaceLayout xl = exact_layout(p);
     const int rc = ws_resolve(src, st, xl.total, &ws);
     if (rc) return rc;
@@ -487,6 +506,8 @@ int run_attention(hipStream_t st, const float *q, const void *k_pool, const void
     // MFMA-bound prefill kernel, which fills the CUs first and leaves its tail
     // to the decode waves.  The no-allocation entry point creates no stream:
     // it runs both kernels in order on the caller's stream.
+    if (no_decode_rows)
+        return launch_prefill(p, head_dim, type_k, max_rows, st) == hipSuccess ? IIAN_PA_OK : IIAN_PA_ERR_HIP;
     if (src.scratch) {
         if (launch_prefill(p, head_dim, type_k, max_rows, st) != hipSuccess) return IIAN_PA_ERR_HIP;
         return launch_decode(p, head_dim, type_k, st) == hipSuccess ? IIAN_PA_OK : IIAN_PA_ERR_HIP;
@@ -595,9 +616,18 @@ int iian_pa_rope_kv_write(void *stream, const float *k_rows, const float *v_rows
     if (rc) return rc;
     rc = row_bytes(type_v, (int64_t) n_head_kv * head_dim_v, vb);
     if (rc) return rc;
-    if ((int64_t) n_head_kv * head_dim > 16384 || (int64_t) n_head_kv * head_dim_v > INT32_MAX / 2 ||
+    if ((int64_t) n_head_kv * head_dim > INT32_MAX / 2 || (int64_t) n_head_kv * head_dim_v > INT32_MAX / 2 ||
         (int64_t) n_head * head_dim > INT32_MAX / 2)
         return IIAN_PA_ERR_ARG;
+    // pairs of adjacent f32 values are loaded and stored as one 8-byte access
+    if (((uintptr_t) k_rows | (uintptr_t) v_rows | (uintptr_t) q_in | (uintptr_t) q_out | (uintptr_t) k_pool |
+         (uintptr_t) v_pool) & 7)
+        return IIAN_PA_ERR_ARG;
+    // a Q8_0 head row is quantised in its own 32-value blocks, staged whole (at most 512 values)
+    if ((type_k == IIAN_PA_TYPE_Q8_0 && (head_dim % 32 || head_dim > 512)) ||
+        (type_v == IIAN_PA_TYPE_Q8_0 && (head_dim_v % 32 || head_dim_v > 512)))
+        return IIAN_PA_ERR_UNSUPPORTED;
+    if (rope->n_dims > 512) return IIAN_PA_ERR_UNSUPPORTED;   // the (cos, sin) table: one pair per thread of 256
     RopeParams p = {};
     p.k_rows = k_rows;
     p.v_rows = v_rows;

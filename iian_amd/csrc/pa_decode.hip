@@ -51,7 +51,8 @@ __global__ __launch_bounds__(64, (D * NRT <= 128) ? 2 : 1) void pa_decode_f16_ke
 // fence per piece costs an L2 write-back).
 template <int D>
 __global__ __launch_bounds__(256) void pa_merge_kernel(AttnParams p) {
-    constexpr int DL = D / 64;   // dims per lane
+    constexpr int DL = (D + 63) / 64;   // dims per lane (head size 96: 2 dims on lanes 0..47)
+    constexpr bool ALL = D % 64 == 0;   // every lane has dims
     const int s = blockIdx.x, hk = blockIdx.y;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int q0 = min(max(p.qsl[s], 0), p.T);
@@ -62,6 +63,7 @@ __global__ __launch_bounds__(256) void pa_merge_kernel(AttnParams p) {
     if (nq <= 0 || M > p.decode_rows || info.y <= 1) return;
     const int hr = grouped ? hk : 0;
     const int rec0 = info.x, ns = info.y;
+    const bool dl_live = ALL || lane * DL < D;
     for (int r = wave; r < M; r += 4) {
         const int t = q0 + r / p.gqa, h = hk * p.gqa + r % p.gqa;
         // the first 8 partial O rows are loaded together with the (m, l) of
@@ -71,7 +73,7 @@ __global__ __launch_bounds__(256) void pa_merge_kernel(AttnParams p) {
         for (int u = 0; u < 8; u++) {
             const float *op = rec_o(p, rec0 + min(u, ns - 1), hr, r, D) + lane * DL;
 #pragma unroll
-            for (int i = 0; i < DL; i++) v0[u][i] = op[i];
+            for (int i = 0; i < DL; i++) v0[u][i] = dl_live ? op[i] : 0.f;
         }
         float2 ml0 = make_float2(-INFINITY, 0.f);
         if (lane < ns) ml0 = *(const float2 *) rec_ml(p, rec0 + lane, hr, r);
@@ -103,7 +105,7 @@ __global__ __launch_bounds__(256) void pa_merge_kernel(AttnParams p) {
                         for (int u = 0; u < 8; u++) {
                             const float *op = rec_o(p, rec0 + c0 + min(j0 + u, nc - 1), hr, r, D) + lane * DL;
 #pragma unroll
-                            for (int i = 0; i < DL; i++) v[u][i] = op[i];
+                            for (int i = 0; i < DL; i++) v[u][i] = dl_live ? op[i] : 0.f;
                         }
                     }
 #pragma unroll
@@ -119,8 +121,9 @@ __global__ __launch_bounds__(256) void pa_merge_kernel(AttnParams p) {
         for (int o = 1; o < 64; o <<= 1) lpart += __shfl_xor(lpart, o);
         const float inv = lpart > 0.f ? 1.f / lpart : 0.f;
         float *out = p.out + ((int64_t) t * p.H + h) * D + lane * DL;
+        if (dl_live)
 #pragma unroll
-        for (int i = 0; i < DL; i++) out[i] = acc[i] * inv;
+            for (int i = 0; i < DL; i++) out[i] = acc[i] * inv;
     }
 }
 
@@ -128,6 +131,7 @@ hipError_t launch_merge(const AttnParams &p, int head_dim, hipStream_t stream) {
     const dim3 grid(p.S, p.Hkv);
     switch (head_dim) {
         case 64: hipLaunchKernelGGL((pa_merge_kernel<64>), grid, dim3(256), 0, stream, p); break;
+        case 96: hipLaunchKernelGGL((pa_merge_kernel<96>), grid, dim3(256), 0, stream, p); break;
         case 128: hipLaunchKernelGGL((pa_merge_kernel<128>), grid, dim3(256), 0, stream, p); break;
         case 256: hipLaunchKernelGGL((pa_merge_kernel<256>), grid, dim3(256), 0, stream, p); break;
         default: return hipErrorInvalidValue;
@@ -296,6 +300,7 @@ hipError_t launch_decode(const AttnParams &p, int head_dim, int kv_type, hipStre
     }
     switch (head_dim) {
         case 64: return nrt == 1 ? launch_decode_t<64, 1>(p, stream) : launch_decode_t<64, 2>(p, stream);
+        case 96: return nrt == 1 ? launch_decode_t<96, 1>(p, stream) : launch_decode_t<96, 2>(p, stream);
         case 128: return nrt == 1 ? launch_decode_t<128, 1>(p, stream) : launch_decode_t<128, 2>(p, stream);
         case 256: return nrt == 1 ? launch_decode_t<256, 1>(p, stream) : launch_decode_t<256, 2>(p, stream);
         default: return hipErrorInvalidValue;

@@ -67,6 +67,9 @@ __device__ __forceinline__ void load_v(const AttnParams &p, const TableWindow &t
             const u32x2 x = stream_load<D>((const u32x2 *) src);
             r.v[e][0] = x[0];
             r.v[e][1] = x[1];
+        } else if constexpr (VW == 3) {   // head size 96: 12-byte slices, 4-byte aligned
+#pragma unroll
+            for (int i = 0; i < 3; i++) r.v[e][i] = stream_load<D>(src + i);
         } else {
 #pragma unroll
             for (int i = 0; i < VW; i += 4) {
@@ -245,10 +248,16 @@ __device__ __forceinline__ void decode_piece(const AttnParams &p, const SeqWindo
                     const int t = w.q0 + r / p.gqa, h = hk * p.gqa + r % p.gqa;
                     const float inv = lr > 0.f ? 1.f / lr : 0.f;
                     float *op = p.out + ((int64_t) t * p.H + h) * D + DPL * n;
+                    if constexpr (DPL % 4 == 0) {
 #pragma unroll
-                    for (int m = 0; m < DPL; m += 4)
-                        *(float4 *) (op + m) = make_float4(o[rt][m][i] * inv, o[rt][m + 1][i] * inv,
-                                                           o[rt][m + 2][i] * inv, o[rt][m + 3][i] * inv);
+                        for (int m = 0; m < DPL; m += 4)
+                            *(float4 *) (op + m) = make_float4(o[rt][m][i] * inv, o[rt][m + 1][i] * inv,
+                                                               o[rt][m + 2][i] * inv, o[rt][m + 3][i] * inv);
+                    } else {   // head size 96: 6 dims per lane, 8-byte aligned
+#pragma unroll
+                        for (int m = 0; m < DPL; m += 2)
+                            *(float2 *) (op + m) = make_float2(o[rt][m][i] * inv, o[rt][m + 1][i] * inv);
+                    }
                 }
             }
         } else {
@@ -260,11 +269,14 @@ __device__ __forceinline__ void decode_piece(const AttnParams &p, const SeqWindo
                     if constexpr (FUSED) {
 #pragma unroll
                         for (int m = 0; m < DPL; m += 2) store_pair_agent(op + m, o[rt][m][i], o[rt][m + 1][i]);
-                    } else {
+                    } else if constexpr (DPL % 4 == 0) {
 #pragma unroll
                         for (int m = 0; m < DPL; m += 4)
                             *(float4 *) (op + m) =
                                 make_float4(o[rt][m][i], o[rt][m + 1][i], o[rt][m + 2][i], o[rt][m + 3][i]);
+                    } else {
+#pragma unroll
+                        for (int m = 0; m < DPL; m += 2) *(float2 *) (op + m) = make_float2(o[rt][m][i], o[rt][m + 1][i]);
                     }
                 }
             }

@@ -188,7 +188,7 @@ class RequestBlocks:
 
 def build_batch(req: RequestBlocks, n_tokens: int, block_size: int, max_blocks: int, num_blocks: int,
                 max_query_len: Optional[int] = None, out: Optional[PagedBatch] = None,
-                err_flag: Optional[torch.Tensor] = None) -> PagedBatch:
+                err_flag: Optional[torch.Tensor] = None, bind: bool = False) -> PagedBatch:
     """The step's PagedBatch built on the device by iian_pa_build_batch from
     the requests' block ids and counts (the work of Engine::step's UBatch
     loop, src/iian/engine.cpp:491-535, without expanding cells on the host).
@@ -215,13 +215,29 @@ def build_batch(req: RequestBlocks, n_tokens: int, block_size: int, max_blocks: 
         _check_batch(out, dev)
     out.max_query_len = int(max_query_len) if max_query_len is not None else out.max_query_len
     out.block_size = block_size
-    st = _lib.load().iian_pa_build_batch(_stream(), req.block_ids.data_ptr(), req.block_off.data_ptr(),
-                                         req.num_computed.data_ptr(), req.n_new.data_ptr(), S, n_tokens, block_size,
-                                         max_blocks, num_blocks, out.block_tables.data_ptr(), out.seq_lens.data_ptr(),
-                                         out.query_start_loc.data_ptr(), out.pos.data_ptr(), out.slots.data_ptr(),
-                                         _ptr(err_flag))
-    _lib.check("iian_pa_build_batch", st)
+    args = (_stream(), req.block_ids.data_ptr(), req.block_off.data_ptr(), req.num_computed.data_ptr(),
+            req.n_new.data_ptr(), S, n_tokens, block_size, max_blocks, num_blocks, out.block_tables.data_ptr(),
+            out.seq_lens.data_ptr(), out.query_start_loc.data_ptr(), out.pos.data_ptr(), out.slots.data_ptr(),
+            _ptr(err_flag))
+    if bind:
+        return out, args
+    _lib.check("iian_pa_build_batch", _lib.load().iian_pa_build_batch(*args))
     return out
+
+
+def bind_build_batch(req: RequestBlocks, n_tokens: int, block_size: int, max_blocks: int, num_blocks: int,
+                     out: PagedBatch, err_flag: Optional[torch.Tensor] = None) -> Callable[[], None]:
+    """build_batch checked once and bound to these buffers and the current
+    stream: the returned function issues iian_pa_build_batch again with one
+    ctypes call, as an engine holding its arguments would."""
+    _, args = build_batch(req, n_tokens, block_size, max_blocks, num_blocks, out=out, err_flag=err_flag, bind=True)
+    fn = _lib.load().iian_pa_build_batch
+
+    def call() -> None:
+        st = fn(*args)
+        if st:
+            _lib.check("iian_pa_build_batch", st)
+    return call
 
 
 def swa_free_blocks(batch: PagedBatch, n_swa: int, clear_table: bool = False) -> torch.Tensor:
@@ -411,7 +427,7 @@ class RopeParams:
 def rope_set_rows_kv(k_pool: KVPool, v_pool: KVPool, k_rows: torch.Tensor, v_rows: torch.Tensor,
                      slots: torch.Tensor, pos: torch.Tensor, rope: RopeParams, n_head_kv: int,
                      q: Optional[torch.Tensor] = None, q_out: Optional[torch.Tensor] = None,
-                     err_flag: Optional[torch.Tensor] = None) -> Optional[torch.Tensor]:
+                     err_flag: Optional[torch.Tensor] = None, bind: bool = False) -> Optional[torch.Tensor]:
     """build_rope on K (and q) fused with the layer's two set_rows calls
     (src/iian/graph.cpp:250-253, 319-320), one launch: k_pool[slots[t]] <-
     rope(k_rows[t], pos[t]), v_pool[slots[t]] <- v_rows[t], and, when q
@@ -451,14 +467,36 @@ def rope_set_rows_kv(k_pool: KVPool, v_pool: KVPool, k_rows: torch.Tensor, v_row
         raise ValueError("freq_factors must be f32 with n_dims/2 values on the rows' device")
     prm = _lib.RopeParams(rope.n_dims, rope.mode, rope.n_ctx_orig, rope.freq_base, rope.freq_scale, rope.ext_factor,
                           rope.attn_factor, rope.beta_fast, rope.beta_slow, _ptr(ff))
+    if bind and not (k_rows.is_contiguous() and v_rows.is_contiguous()):
+        raise ValueError("bound rows must be contiguous")
     k_rows, v_rows = k_rows.contiguous(), v_rows.contiguous()
-    st = _lib.load().iian_pa_rope_kv_write(_stream(), k_rows.data_ptr(), v_rows.data_ptr(), _ptr(q), _ptr(q_out),
-                                           pos.data_ptr(), slots.data_ptr(), T, H, n_head_kv, D,
-                                           v_pool.n_embd // n_head_kv, C.byref(prm), k_pool.data.data_ptr(),
-                                           v_pool.data.data_ptr(), k_pool.n_cells, k_pool.type, v_pool.type,
-                                           _ptr(err_flag))
-    _lib.check("iian_pa_rope_kv_write", st)
+    args = (_stream(), k_rows.data_ptr(), v_rows.data_ptr(), _ptr(q), _ptr(q_out), pos.data_ptr(), slots.data_ptr(),
+            T, H, n_head_kv, D, v_pool.n_embd // n_head_kv, C.byref(prm), k_pool.data.data_ptr(),
+            v_pool.data.data_ptr(), k_pool.n_cells, k_pool.type, v_pool.type, _ptr(err_flag))
+    if bind:
+        return q_out, (args, prm)
+    _lib.check("iian_pa_rope_kv_write", _lib.load().iian_pa_rope_kv_write(*args))
     return q_out
+
+
+def bind_rope_set_rows_kv(k_pool: KVPool, v_pool: KVPool, k_rows: torch.Tensor, v_rows: torch.Tensor,
+                          slots: torch.Tensor, pos: torch.Tensor, rope: RopeParams, n_head_kv: int,
+                          q: Optional[torch.Tensor] = None, q_out: Optional[torch.Tensor] = None,
+                          err_flag: Optional[torch.Tensor] = None) -> Callable[[], None]:
+    """rope_set_rows_kv checked once and bound to these buffers (contiguous
+    rows; q_out given when q is) and the current stream, as bind_paged_attn."""
+    if q is not None and q_out is None:
+        raise ValueError("a bound call needs q_out when q is given")
+    _, (args, prm) = rope_set_rows_kv(k_pool, v_pool, k_rows, v_rows, slots, pos, rope, n_head_kv, q=q, q_out=q_out,
+                                      err_flag=err_flag, bind=True)
+    fn = _lib.load().iian_pa_rope_kv_write
+
+    def call() -> None:
+        st = fn(*args)
+        if st:
+            _lib.check("iian_pa_rope_kv_write", st)
+    call.params = prm   # the rope parameter block the bound arguments point at
+    return call
 
 
 def workspace_size(n_tokens: int, n_seqs: int, n_head: int, n_head_kv: int, head_dim_v: int, max_blocks: int,

@@ -242,8 +242,12 @@ typedef struct {
  * rotated with each product rounded; cos and sin are the correctly rounded
  * fp32 values of the fp32 angle, where ggml calls libm cosf / sinf (which can
  * differ in the last bit).  Conversions, slot rules and *err_flag bit 0 as
- * iian_pa_kv_write; q is rotated whatever the slot.  Returns
- * IIAN_PA_ERR_UNSUPPORTED for other rope modes. */
+ * iian_pa_kv_write; q is rotated whatever the slot.  Rows, q and the pools
+ * must be 8-byte aligned (IIAN_PA_ERR_ARG otherwise).  Returns
+ * IIAN_PA_ERR_UNSUPPORTED for other rope modes, for n_dims above 512, and
+ * for a Q8_0 pool whose head size is not a multiple of 32 or is above 512
+ * (each head's values are quantised in their own 32-value blocks, as
+ * iian_pa_supported requires). */
 int iian_pa_rope_kv_write(void *stream, const float *k_rows, const float *v_rows, const float *q_in,
                           float *q_out, const int32_t *pos, const int64_t *slots, int64_t n_rows,
                           int32_t n_head, int32_t n_head_kv, int32_t head_dim, int32_t head_dim_v,

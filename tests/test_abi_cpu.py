@@ -275,3 +275,26 @@ def test_runtime_layer_checks_the_step_shapes():
             rt.layer(a["q"], a["kr"], a["vr"], pool, pool, prm, a["out"])
     with pytest.raises(ValueError, match="GPU"):   # right shapes, host tensors
         rt.layer(q, kr, vr, pool, pool, prm, out)
+
+
+def test_rope_kv_write_rejects_unaligned_rows_and_split_q8_blocks(lib):
+    """iian_pa_rope_kv_write loads and stores adjacent f32 pairs as 8-byte
+    accesses and quantises each Q8_0 head row in its own blocks: unaligned
+    buffers and Q8_0 heads that are not whole 32-value blocks (or above 512
+    values) are refused on the host (fake pointers: nothing may reach the
+    device)."""
+    from iian_amd import _lib
+    prm = _lib.RopeParams(64, 0, 0, 10000.0, 1.0, 0.0, 1.0, 32.0, 1.0, None)
+    f = lib.iian_pa_rope_kv_write
+
+    def call(k_rows=0x1000, q=0x3000, D=64, Dv=64, tk=1, tv=1):
+        return f(None, k_rows, 0x2000, q, q, 0x4000, 0x5000, 4, 4, 2, D, Dv, C.byref(prm), 0x6000, 0x7000, 64, tk,
+                 tv, None)
+    assert call(k_rows=0x1004) == _lib.ERR_ARG
+    assert call(q=0x3004) == _lib.ERR_ARG
+    assert call(D=80, Dv=64, tk=8, tv=1) == _lib.ERR_UNSUPPORTED     # 80-value heads: blocks would span heads
+    assert call(D=64, Dv=48, tk=1, tv=8) == _lib.ERR_UNSUPPORTED
+    assert call(D=576, Dv=64, tk=8, tv=1) == _lib.ERR_UNSUPPORTED
+    wide = _lib.RopeParams(576, 0, 0, 10000.0, 1.0, 0.0, 1.0, 32.0, 1.0, None)   # more pairs than the table holds
+    assert f(None, 0x1000, 0x2000, 0x3000, 0x3000, 0x4000, 0x5000, 4, 4, 2, 640, 64, C.byref(wide), 0x6000, 0x7000,
+             64, 1, 1, None) == _lib.ERR_UNSUPPORTED

@@ -38,7 +38,7 @@ GENERAL = {
     "f32_mixed_d64": (14, 2, 64, [900, 1500, 64], [128, 1, 1], {"k_type": F32}),
     "f16k_f32v_decode": (32, 8, 128, [700, 101, 4101], [1, 5, 1], {"k_type": F16, "v_type": F32}),
     "f32k_f16v_prefill": (8, 2, 128, [500, 90], [200, 1], {"k_type": F32, "v_type": F16}),
-    "phi3_d96_decode": (32, 32, 96, [800, 1200, 70], [1, 1, 1], {}),
+    "phi3_d96_decode_f32": (32, 32, 96, [800, 1200, 70], [1, 1, 1], {"k_type": F32}),   # f16 decode: MFMA kernel
     "phi3_d96_prefill_gqa4": (40, 10, 96, [700, 300], [256, 33], {}),
     "d80_f16_mixed": (16, 4, 80, [600, 64, 900], [100, 1, 1], {}),
     "d80_f32_decode": (8, 8, 80, [300, 1000], [1, 1], {"k_type": F32}),

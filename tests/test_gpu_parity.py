@@ -188,6 +188,13 @@ SMALL = {
     "q8_mixed_prefill_decode": (32, 8, 128, [900, 1500, 700, 64], [256, 1, 1, 64], {"k_type": Q8_0}),
     "q8_swa_prefill": (16, 8, 256, [2000, 1200], [256, 100], {"k_type": Q8_0, "n_swa": 512}),
     "q8_prefill_softcap": (8, 2, 128, [333, 77], [1, 40], {"k_type": Q8_0, "softcap": 30.0}),
+    # head size 96 (Phi-3) f16 decode and spec-verify on the MFMA decode kernel: 12-byte V
+    # slices, 6 output dims per lane, the merge's 48 live lanes
+    "d96_decode_gqa1": (32, 32, 96, [800, 1200, 70, 4000], [1, 1, 1, 1], {}),
+    "d96_decode_gqa4_splits": (32, 8, 96, [9000, 513, 77], [1, 1, 1], {}),
+    "d96_spec_verify_5": (32, 8, 96, [700, 101, 4101], [5, 5, 5], {}),
+    "d96_swa_softcap": (16, 4, 96, [3000, 900], [1, 2], {"n_swa": 700, "softcap": 30.0}),
+    "d96_random_positions_bs32": (8, 2, 96, [600, 300], [6, 3], {"pos_mode": "random", "bs": 32}),
     # spec-verify launch (rows per kv head up to 32) holding sequences of 4 and 8 rows too
     "mixed_rows": (32, 8, 128, [600, 90, 1500], [1, 5, 2], {}),
     "q8_mixed_rows": (32, 8, 128, [600, 90, 1500], [1, 5, 2], {"k_type": Q8_0}),
@@ -345,17 +352,18 @@ def test_segment_window_decode_matches_stream_k(pa, oracle, name):
     assert row_rel_err(seg, sk).max() <= TOL
 
 
-@pytest.mark.parametrize("k_type,nq", [(F16, 1), (F16, 5), (F16, 64), (Q8_0, 1), (Q8_0, 5), (Q8_0, 64)])
-def test_attention_growing_scores(pa, oracle, k_type, nq):
+@pytest.mark.parametrize("k_type,nq,D", [(F16, 1, 128), (F16, 5, 128), (F16, 64, 128), (Q8_0, 1, 128), (Q8_0, 5, 128),
+                                        (Q8_0, 64, 128), (F16, 1, 96), (F16, 5, 96)])
+def test_attention_growing_scores(pa, oracle, k_type, nq, D):
     """K rows scaled by a ramp 1 .. 16 along each sequence, so every row's
     running max keeps rising by many log2 units: exercises the online-softmax
     rescale of O and l on most tiles (random N(0,1) data barely moves the max
     after the first tile), and peaked softmax rows whose scores a single f16 q
     would get wrong by more than the tolerance.  nq = 1, 5: decode and
     spec-verify kernels; nq = 64: prefill kernel."""
-    banner(f"growing scores k_type={k_type} nq={nq}")
+    banner(f"growing scores k_type={k_type} nq={nq} D={D}")
     rng = np.random.default_rng(46 + nq + k_type)
-    c = make_case(rng, 32, 8, 128, [1300, 2100, 90], [nq] * 3, k_type=k_type, quantize=oracle.quantize_q8_0)
+    c = make_case(rng, 32, 8, D, [1300, 2100, 90], [nq] * 3, k_type=k_type, quantize=oracle.quantize_q8_0)
     n_embd = c.Hkv * c.D
     rows = decode_rows_f64(c.k_pool, c.k_type, n_embd).astype(np.float32)
     for s in range(len(c.seq_lens)):
@@ -630,7 +638,7 @@ def config_parity(pa, oracle, name, n_items=None, seed=None):
 @pytest.mark.parametrize("name,n_items", [
     ("cfg1", None), ("cfg2", None), ("cfg3", 4096), ("cfg3_prefill", 4096), ("cfg3_p0", 4096), ("cfg4", 2048),
     ("cfg5_global_decode", None), ("cfg5_local_decode", None),
-    ("cfg5_global_prefill", 1024), ("cfg5_local_prefill", 1024),
+    ("cfg5_global_prefill", 1024), ("cfg5_local_prefill", 1024), ("phi3_decode", None),
 ])
 def test_config_parity(pa, oracle, name, n_items):
     config_parity(pa, oracle, name, n_items)
