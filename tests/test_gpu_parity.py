@@ -170,6 +170,11 @@ SMALL = {
     # blocks in reverse (a round that 12 does not divide)
     "prefill_nrb12_reversed": (32, 8, 128, [600, 500, 450, 700], [384, 384, 384, 384], {}),
     "random_positions": (8, 2, 64, [300, 200], [6, 40], {"pos_mode": "random"}),
+    # prefill row blocks split in two KV halves: chunks with no prior context,
+    # whose first row blocks see one tile (the first half attends nothing), and
+    # a batch with more row blocks than one round of slots (not split)
+    "prefill_split_p0_d128": (32, 8, 128, [40, 300, 1000], [40, 300, 1], {}),
+    "prefill_unsplit_many_rb_d64": (14, 2, 64, [700] * 8 + [900, 50], [600] * 8 + [1, 1], {}),
     # Q8_0 pools (decode / spec-verify kernel)
     "q8_decode_gqa4_d128": (32, 8, 128, [513, 77, 2048, 33], [1, 1, 1, 1], {"k_type": Q8_0}),
     "q8_spec_verify_5": (32, 8, 128, [700, 101, 4101], [5, 5, 5], {"k_type": Q8_0}),
