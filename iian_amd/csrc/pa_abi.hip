@@ -40,6 +40,10 @@ constexpr int kF16DecodeWavesPerCu = 6;
 // against 162.2 us; 1 per CU 205.6 us, 3 per CU 185.8 us).
 constexpr int kF16MixedDecodeWavesPerCu = 2;
 constexpr int kF16DecodeWavesPerCuD256 = 3;
+// Head pairs at head size 96 (two kv heads per wave, twice the bytes per
+// unit of work): 4 waves per CU measured best at Phi-3.5 shapes (414 us
+// against 420 at 3, 426 at 6, 455 at 2).
+constexpr int kF16DecodeWavesPerCuPairs = 4;
 constexpr int kQ8DecodeWavesPerCu = 8;
 constexpr int kMaxWavesPerCu = kQ8DecodeWavesPerCu;
 constexpr int kDefaultCus = 256;   // an MI355X, when the device cannot be queried
@@ -108,7 +112,7 @@ WorkspaceLayout exact_layout(const AttnParams &p) {
     WorkspaceLayout l;
     l.o = 0;
     l.ml = align256(records * (size_t) p.rec_stride * sizeof(float));
-    l.seg = l.ml + align256(records * p.rec_heads * p.decode_rows * 2 * sizeof(float));
+    l.seg = l.ml + align256(records * p.rec_heads * p.rec_rows * 2 * sizeof(float));
     l.ctr = l.seg + align256(nseg * sizeof(int2));
     l.total = l.ctr + align256((size_t) p.S * p.Hkv * sizeof(uint64_t));
     return l;
@@ -441,6 +445,15 @@ int run_attention(hipStream_t st, const float *q, const void *k_pool, const void
     // the prefill kernel.
     const int max_rows = max_query_len * p.gqa;
     p.decode_rows = (max_rows > 16 && max_rows <= kDecodeRowsMax) ? kDecodeRowsMax : 16;
+    // f16 decode at head size 96: one wave per pair of kv heads (their slices
+    // of a cell row are three whole 128-byte lines; one head's slice shares a
+    // line with its neighbour's) when every sequence has at most 8 rows per kv
+    // head, so that a pair's rows fill one 16-row tile
+    p.head_group = 1;
+    if (decode96 && max_rows <= 8 && n_head_kv % 2 == 0) {
+        p.head_group = 2;
+        p.decode_rows = 8;
+    }
 
     if (type_k == IIAN_PA_TYPE_Q8_0) {
         p.rec_heads = n_head_kv;
@@ -448,8 +461,10 @@ int run_attention(hipStream_t st, const float *q, const void *k_pool, const void
     } else {
         p.rec_heads = 1;
         p.sk_workers = (head_dim == 256 ? kF16DecodeWavesPerCuD256 : kF16DecodeWavesPerCu) * cus;
+        if (p.head_group == 2) p.sk_workers = kF16DecodeWavesPerCuPairs * cus;
     }
-    p.rec_stride = (int64_t) p.rec_heads * p.decode_rows * head_dim_v + kRecordPad;
+    p.rec_rows = p.decode_rows * p.head_group;
+    p.rec_stride = (int64_t) p.rec_heads * p.rec_rows * head_dim_v + kRecordPad;
     const bool decode_only = max_rows <= p.decode_rows;
     // f16 decode calls with short or window-bounded segments: one workgroup
     // per (sequence, kv head) attends and merges in LDS, in one launch

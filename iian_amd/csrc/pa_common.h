@@ -55,6 +55,8 @@ struct AttnParams {
     int32_t rec_heads;          // kv heads per partial record: 1, or Hkv for grouped workers
     int32_t seg_waves;          // > 0: f16 decode by pa_decode_seg_kernel, seg_waves waves per segment
     int32_t cus_per_xcd;        // CUs per XCD: workgroups b and b + 8*cus_per_xcd of a launch share a CU
+    int32_t head_group;         // kv heads per f16 decode segment: 1, or 2 (head size 96, rows per head <= 8)
+    int32_t rec_rows;           // rows of a partial record per kv-head slot: decode_rows * head_group
 };
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -166,7 +168,7 @@ struct Piece {
 template <bool GROUPED, typename Body>
 __device__ __forceinline__ void for_each_piece(const AttnParams &p, int worker, int hk_fixed, Body &&body) {
     const int lane = threadIdx.x & 63;
-    const int unit = GROUPED ? 1 : p.Hkv;
+    const int unit = GROUPED ? 1 : p.Hkv / p.head_group;   // segments per sequence
     // lanes hold the tile counts of sequences base + lane and their inclusive
     // prefix along the line; a piece's window is re-read with scalar loads
     // (keeping every field in lanes costs registers the tile loop needs)
@@ -209,7 +211,7 @@ __device__ __forceinline__ void for_each_piece(const AttnParams &p, int worker, 
         pc.t0 = GROUPED ? off : off % w.nt;
         pc.t1 = min(w.nt, pc.t0 + (end - start));
         const int seg_start = excl + (GROUPED ? 0 : pc.hk * w.nt);
-        pc.seg = GROUPED ? s : s * p.Hkv + pc.hk;
+        pc.seg = GROUPED ? s : s * unit + pc.hk;
         pc.rec = worker + pc.seg;
         pc.rec0 = seg_start / per + pc.seg;   // record of the segment's first piece
         pc.pieces = (seg_start + w.nt - 1) / per - seg_start / per + 1;
@@ -221,10 +223,10 @@ __device__ __forceinline__ void for_each_piece(const AttnParams &p, int worker, 
 
 // Partial record row r of kv head slot hr (0, or the kv head for grouped workers).
 __device__ __forceinline__ float *rec_o(const AttnParams &p, int rec, int hr, int r, int dv) {
-    return p.part_o + (int64_t) rec * p.rec_stride + ((int64_t) hr * p.decode_rows + r) * dv;
+    return p.part_o + (int64_t) rec * p.rec_stride + ((int64_t) hr * p.rec_rows + r) * dv;
 }
 __device__ __forceinline__ float *rec_ml(const AttnParams &p, int rec, int hr, int r) {
-    return p.part_ml + (((int64_t) rec * p.rec_heads + hr) * p.decode_rows + r) * 2;
+    return p.part_ml + (((int64_t) rec * p.rec_heads + hr) * p.rec_rows + r) * 2;
 }
 
 // ---- Merge of a split segment inside the launch (mixed prefill launch) ----

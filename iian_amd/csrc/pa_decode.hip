@@ -38,9 +38,11 @@ namespace iian_pa {
 // 1.5 waves per SIMD are launched at D <= 128 (kF16DecodeWaves in pa_abi.hip),
 // within a register budget of two waves per SIMD up to D*NRT = 128 (a budget
 // of one wave per SIMD measured slower).
-template <int D, int NRT>
+template <int D, int NRT, int HG = 1>
 __global__ __launch_bounds__(64, (D * NRT <= 128) ? 2 : 1) void pa_decode_f16_kernel(AttnParams p) {
-    for_each_piece<false>(p, blockIdx.x, 0, [&](const SeqWindow &w, const Piece &pc) { decode_piece<D, NRT>(p, w, pc); });
+    for_each_piece<false>(p, blockIdx.x, 0, [&](const SeqWindow &w, const Piece &pc) {
+        decode_piece<D, NRT, false, false, HG>(p, w, pc);
+    });
 }
 
 // Log-sum-exp merge of the stream-K partials: one workgroup per (sequence, kv
@@ -53,19 +55,22 @@ template <int D>
 __global__ __launch_bounds__(256) void pa_merge_kernel(AttnParams p) {
     constexpr int DL = (D + 63) / 64;   // dims per lane (head size 96: 2 dims on lanes 0..47)
     constexpr bool ALL = D % 64 == 0;   // every lane has dims
-    const int s = blockIdx.x, hk = blockIdx.y;
+    // blockIdx.y: the kv head, or the head group of head_group kv heads
+    // (rows r of a group's segment: row r % M of its head r / M)
+    const int s = blockIdx.x, hg = blockIdx.y;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int q0 = min(max(p.qsl[s], 0), p.T);
     const int nq = min(max(p.qsl[s + 1], q0), p.T) - q0;
     const int M = nq * p.gqa;
     const bool grouped = p.rec_heads > 1;
-    const int2 info = p.seg_info[grouped ? s : s * p.Hkv + hk];
+    const int2 info = p.seg_info[grouped ? s : s * (p.Hkv / p.head_group) + hg];
     if (nq <= 0 || M > p.decode_rows || info.y <= 1) return;
-    const int hr = grouped ? hk : 0;
+    const int hr = grouped ? hg : 0;
     const int rec0 = info.x, ns = info.y;
     const bool dl_live = ALL || lane * DL < D;
-    for (int r = wave; r < M; r += 4) {
-        const int t = q0 + r / p.gqa, h = hk * p.gqa + r % p.gqa;
+    for (int r = wave; r < M * p.head_group; r += 4) {
+        const int hl = r / M, rh = r - hl * M;
+        const int t = q0 + rh / p.gqa, h = (hg * p.head_group + hl) * p.gqa + rh % p.gqa;
         // the first 8 partial O rows are loaded together with the (m, l) of
         // pieces lane, lane + 64, ...; the first (m, l) chunk stays in registers
         float v0[8][DL];
@@ -128,7 +133,7 @@ __global__ __launch_bounds__(256) void pa_merge_kernel(AttnParams p) {
 }
 
 hipError_t launch_merge(const AttnParams &p, int head_dim, hipStream_t stream) {
-    const dim3 grid(p.S, p.Hkv);
+    const dim3 grid(p.S, p.Hkv / p.head_group);
     switch (head_dim) {
         case 64: hipLaunchKernelGGL((pa_merge_kernel<64>), grid, dim3(256), 0, stream, p); break;
         case 96: hipLaunchKernelGGL((pa_merge_kernel<96>), grid, dim3(256), 0, stream, p); break;
@@ -272,9 +277,9 @@ __global__ __launch_bounds__(64 * NW) void pa_decode_seg_kernel(AttnParams p) {
     }
 }
 
-template <int D, int NRT>
+template <int D, int NRT, int HG = 1>
 static hipError_t launch_decode_t(const AttnParams &p, hipStream_t stream) {
-    hipLaunchKernelGGL((pa_decode_f16_kernel<D, NRT>), dim3(p.sk_workers), dim3(64), 0, stream, p);
+    hipLaunchKernelGGL((pa_decode_f16_kernel<D, NRT, HG>), dim3(p.sk_workers), dim3(64), 0, stream, p);
     const hipError_t e = hipGetLastError();
     return e != hipSuccess ? e : launch_merge(p, D, stream);
 }
@@ -282,6 +287,7 @@ static hipError_t launch_decode_t(const AttnParams &p, hipStream_t stream) {
 hipError_t launch_decode(const AttnParams &p, int head_dim, int kv_type, hipStream_t stream) {
     if (kv_type == 8) return launch_decode_q8(p, head_dim, stream);
     if (kv_type != 1) return hipErrorInvalidValue;
+    if (p.head_group != 1 && head_dim != 96) return hipErrorInvalidValue;
     const int nrt = p.decode_rows > 16 ? 2 : 1;
     if (p.seg_waves > 0) {
         if (nrt != 1) return hipErrorInvalidValue;
@@ -300,7 +306,9 @@ hipError_t launch_decode(const AttnParams &p, int head_dim, int kv_type, hipStre
     }
     switch (head_dim) {
         case 64: return nrt == 1 ? launch_decode_t<64, 1>(p, stream) : launch_decode_t<64, 2>(p, stream);
-        case 96: return nrt == 1 ? launch_decode_t<96, 1>(p, stream) : launch_decode_t<96, 2>(p, stream);
+        case 96:
+            if (p.head_group == 2) return nrt == 1 ? launch_decode_t<96, 1, 2>(p, stream) : hipErrorInvalidValue;
+            return nrt == 1 ? launch_decode_t<96, 1>(p, stream) : launch_decode_t<96, 2>(p, stream);
         case 128: return nrt == 1 ? launch_decode_t<128, 1>(p, stream) : launch_decode_t<128, 2>(p, stream);
         case 256: return nrt == 1 ? launch_decode_t<256, 1>(p, stream) : launch_decode_t<256, 2>(p, stream);
         default: return hipErrorInvalidValue;

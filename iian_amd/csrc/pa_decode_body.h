@@ -10,15 +10,18 @@ namespace iian_pa {
 
 // K/V are read once per call: non-temporal loads keep them from evicting the
 // block tables and partials.  Measured on MI355X: +5% at D=128 (256-byte head
-// slices), -7% at D=256, so it is chosen per head size.
-template <int D>
+// slices), -7% at D=256, so it is chosen per head size.  Head pairs at D = 96
+// (HG = 2) load cached: a pair's three lines are requested by two load
+// instructions each (one per head), and a cached line serves the second
+// (Phi-3.5 shapes: 414 against 434 us, HBM traffic 1.12x -> the lines once).
+template <int D, int HG = 1>
 struct KvStream {
-    static constexpr bool kNonTemporal = D <= 128;
+    static constexpr bool kNonTemporal = D <= 128 && HG == 1;
 };
 
-template <int D, typename T>
+template <bool NT, typename T>
 __device__ __forceinline__ T stream_load(const T *ptr) {
-    if constexpr (KvStream<D>::kNonTemporal)
+    if constexpr (NT)
         return __builtin_nontemporal_load(ptr);
     else
         return *ptr;
@@ -34,7 +37,7 @@ struct VRegs {
 };
 
 // K: lane (n, g) loads cells tile + 8*(n/4) + 4h + (n%4), dims 32ks + 8g .. +8
-template <int D>
+template <int D, bool NT>
 __device__ __forceinline__ void load_k(const AttnParams &p, const TableWindow &tw, int L, int hk, int tile,
                                        KRegs<D> &r) {
     const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
@@ -46,12 +49,12 @@ __device__ __forceinline__ void load_k(const AttnParams &p, const TableWindow &t
         const uint32_t row = table_row(p, tw, grp, c);
         const char *base = p.k_pool + pool_off(row, p.k_row) + (hk * D * 2 + g * 16);
 #pragma unroll
-        for (int ks = 0; ks < D / 32; ks++) r.k[h][ks] = stream_load<D>((const u32x4 *) (base + ks * 64));
+        for (int ks = 0; ks < D / 32; ks++) r.k[h][ks] = stream_load<NT>((const u32x4 *) (base + ks * 64));
     }
 }
 
 // V: lane (n, g) loads cells tile + 8g + e, dims (D/16)*n .. +D/16
-template <int D>
+template <int D, bool NT>
 __device__ __forceinline__ void load_v(const AttnParams &p, const TableWindow &tw, int L, int hk, int tile,
                                        VRegs<D> &r) {
     constexpr int VW = D / 32;
@@ -64,16 +67,16 @@ __device__ __forceinline__ void load_v(const AttnParams &p, const TableWindow &t
         const uint32_t row = table_row(p, tw, grp, c);
         const uint32_t *src = (const uint32_t *) (p.v_pool + pool_off(row, p.v_row) + (hk * D * 2 + n * (D / 8)));
         if constexpr (VW == 2) {
-            const u32x2 x = stream_load<D>((const u32x2 *) src);
+            const u32x2 x = stream_load<NT>((const u32x2 *) src);
             r.v[e][0] = x[0];
             r.v[e][1] = x[1];
         } else if constexpr (VW == 3) {   // head size 96: 12-byte slices, 4-byte aligned
 #pragma unroll
-            for (int i = 0; i < 3; i++) r.v[e][i] = stream_load<D>(src + i);
+            for (int i = 0; i < 3; i++) r.v[e][i] = stream_load<NT>(src + i);
         } else {
 #pragma unroll
             for (int i = 0; i < VW; i += 4) {
-                const u32x4 x = stream_load<D>((const u32x4 *) (src + i));
+                const u32x4 x = stream_load<NT>((const u32x4 *) (src + i));
                 r.v[e][i] = x[0];
                 r.v[e][i + 1] = x[1];
                 r.v[e][i + 2] = x[2];
@@ -89,15 +92,27 @@ __device__ __forceinline__ void load_v(const AttnParams &p, const TableWindow &t
 // table window comes loaded (*tw_pre, covering the piece's first tile), and the
 // piece's record goes to the wave's LDS record lrec (O rows at lrec[r*D + d],
 // (m, l) of row r at lrec[16*D + 2r]) for a merge inside the workgroup.
-template <int D, int NRT, bool FUSED = false, bool LREC = false>
+// HG = 2 (head size 96): the piece covers kv heads 2*pc.hk and 2*pc.hk + 1,
+// whose 192-byte slices of a cell row are three whole 128-byte lines, where
+// one head's slice shares a line with its neighbour's (one head per wave
+// fetched those lines once per head: 4/3 of the bytes).  Row r < 2M of the
+// tile is row r % M of head r / M (M <= 8 rows per head); QK^T and PV run once
+// per head, each on the other head's rows too, and each lane keeps the head
+// of its own row.
+template <int D, int NRT, bool FUSED = false, bool LREC = false, int HG = 1>
 __device__ __forceinline__ void decode_piece(const AttnParams &p, const SeqWindow &w, const Piece &pc,
                                              float *lrec = nullptr, const TableWindow *tw_pre = nullptr) {
     static_assert(!LREC || (NRT == 1 && !FUSED), "LDS records hold one 16-row tile");
+    static_assert(HG == 1 || (HG == 2 && NRT == 1 && !FUSED && !LREC), "head pairs: one 16-row tile, merge launch");
     constexpr int KS = D / 32;
     constexpr int DPL = D / 16;
+    constexpr bool NT = KvStream<D, HG>::kNonTemporal;
     const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
-    const int s = pc.s, hk = pc.hk;
-    const int M = w.nq * p.gqa;
+    const int s = pc.s, hk = pc.hk * HG;   // (first) kv head of the piece
+    const int M = w.nq * p.gqa;            // rows per kv head
+    // kv head slot (0 or 1) and row within its head of tile row r
+    auto row_head = [&](int r) { return HG == 1 ? 0 : (r >= M ? 1 : 0); };
+    auto row_in_head = [&](int r) { return HG == 1 ? r : (r >= M ? r - M : r); };
     const int cb = w.c_lo + pc.t0 * kTile;
     const int ce = min(w.c_hi, w.c_lo + pc.t1 * kTile);
 
@@ -114,8 +129,9 @@ __device__ __forceinline__ void decode_piece(const AttnParams &p, const SeqWindo
     for (int rt = 0; rt < NRT; rt++) {
         const int r = rt * 16 + n;
         prow[rt] = w.pmax;
-        if (r < M) {
-            const int t = w.q0 + r / p.gqa, h = hk * p.gqa + r % p.gqa;
+        if (r < HG * M) {
+            const int rh = row_in_head(r);
+            const int t = w.q0 + rh / p.gqa, h = (hk + row_head(r)) * p.gqa + rh % p.gqa;
             prow[rt] = p.pos[t];
             const float *qp = p.q + ((int64_t) t * p.H + h) * D + 8 * g;
 #pragma unroll
@@ -133,33 +149,47 @@ __device__ __forceinline__ void decode_piece(const AttnParams &p, const SeqWindo
         for (int m = 0; m < DPL; m++) o[rt][m] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
+    const bool own1 = HG > 1 && row_head(n) == 1;   // this lane's row (column of S^T, row of P) is of head slot 1
     if (cb < ce) {
-        KRegs<D> kr;
-        VRegs<D> vr;
-        load_k<D>(p, tw, w.L, hk, cb, kr);
-        load_v<D>(p, tw, w.L, hk, cb, vr);
+        KRegs<D> kr[HG];
+        VRegs<D> vr[HG];
+#pragma unroll
+        for (int i = 0; i < HG; i++) load_k<D, NT>(p, tw, w.L, hk + i, cb, kr[i]);
+#pragma unroll
+        for (int i = 0; i < HG; i++) load_v<D, NT>(p, tw, w.L, hk + i, cb, vr[i]);
         for (int tile = cb; tile < ce; tile += kTile) {
             const int next = tile + kTile;
             const bool has_next = next < ce;
             if (has_next && ((min(next + kTile - 1, w.L - 1) >> p.bs_log2) - tw.first) >= 64)
                 table_load(p, s, next >> p.bs_log2, w.L, tw);   // pieces longer than 64 blocks
 
-            // S^T = K Q^T for every row tile
+            // S^T = K Q^T for every row tile (per kv head slot; a lane keeps
+            // the scores of its own row's head)
             f32x4 sacc[NRT][2];
 #pragma unroll
             for (int rt = 0; rt < NRT; rt++)
 #pragma unroll
                 for (int h = 0; h < 2; h++) {
-                    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+                    f32x4 acc[HG];
 #pragma unroll
-                    for (int ks = 0; ks < KS; ks++) {
-                        const f16x8 a = __builtin_bit_cast(f16x8, kr.k[h][ks]);
-                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qh[rt][ks], acc, 0, 0, 0);
-                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ql[rt][ks], acc, 0, 0, 0);
+                    for (int i = 0; i < HG; i++) {
+                        acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                        for (int ks = 0; ks < KS; ks++) {
+                            const f16x8 a = __builtin_bit_cast(f16x8, kr[i].k[h][ks]);
+                            acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qh[rt][ks], acc[i], 0, 0, 0);
+                            acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ql[rt][ks], acc[i], 0, 0, 0);
+                        }
                     }
-                    sacc[rt][h] = acc;
+                    sacc[rt][h] = acc[0];
+                    if constexpr (HG > 1) {
+#pragma unroll
+                        for (int e = 0; e < 4; e++) sacc[rt][h][e] = own1 ? acc[HG - 1][e] : acc[0][e];
+                    }
                 }
-            if (has_next) load_k<D>(p, tw, w.L, hk, next, kr);
+            if (has_next)
+#pragma unroll
+                for (int i = 0; i < HG; i++) load_k<D, NT>(p, tw, w.L, hk + i, next, kr[i]);
 
             // online softmax; P becomes the A operand of PV
             const bool full = tile + kTile <= w.L && (!p.causal || tile + kTile - 1 <= w.pmin) &&
@@ -214,22 +244,32 @@ __device__ __forceinline__ void decode_piece(const AttnParams &p, const SeqWindo
                 pa[rt] = __builtin_bit_cast(f16x8, pk);
             }
 
-            // V^T B operands: MFMA m takes dim DPL*n + m of cells 8g .. 8g+7
-            u32x4 vb[DPL];
+            // V^T B operands: MFMA m takes dim DPL*n + m of cells 8g .. 8g+7;
+            // head slot by head slot, each slot's next V loads reusing its
+            // registers as soon as its operands are built.  With head pairs,
+            // slot i's PV takes P of slot i's rows only (the A operand row is
+            // this lane's row).
+            const f16x8 zero = __builtin_bit_cast(f16x8, u32x4{0u, 0u, 0u, 0u});
 #pragma unroll
-            for (int m = 0; m < DPL; m++) {
-                const uint32_t sel = (m & 1) ? 0x07060302u : 0x05040100u;
+            for (int i = 0; i < HG; i++) {
+                u32x4 vb[DPL];
 #pragma unroll
-                for (int wi = 0; wi < 4; wi++)
-                    vb[m][wi] = __builtin_amdgcn_perm(vr.v[2 * wi + 1][m >> 1], vr.v[2 * wi][m >> 1], sel);
+                for (int m = 0; m < DPL; m++) {
+                    const uint32_t sel = (m & 1) ? 0x07060302u : 0x05040100u;
+#pragma unroll
+                    for (int wi = 0; wi < 4; wi++)
+                        vb[m][wi] = __builtin_amdgcn_perm(vr[i].v[2 * wi + 1][m >> 1], vr[i].v[2 * wi][m >> 1], sel);
+                }
+                if (has_next) load_v<D, NT>(p, tw, w.L, hk + i, next, vr[i]);
+#pragma unroll
+                for (int m = 0; m < DPL; m++)
+#pragma unroll
+                    for (int rt = 0; rt < NRT; rt++) {
+                        const f16x8 pi = HG == 1 ? pa[rt] : ((own1 == (i == 1)) ? pa[rt] : zero);
+                        o[rt][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pi, __builtin_bit_cast(f16x8, vb[m]), o[rt][m],
+                                                                          0, 0, 0);
+                    }
             }
-            if (has_next) load_v<D>(p, tw, w.L, hk, next, vr);
-#pragma unroll
-            for (int m = 0; m < DPL; m++)
-#pragma unroll
-                for (int rt = 0; rt < NRT; rt++)
-                    o[rt][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[rt], __builtin_bit_cast(f16x8, vb[m]),
-                                                                      o[rt][m], 0, 0, 0);
         }
     }
 
@@ -244,8 +284,9 @@ __device__ __forceinline__ void decode_piece(const AttnParams &p, const SeqWindo
             for (int i = 0; i < 4; i++) {
                 const int r = rt * 16 + 4 * g + i;
                 const float lr = __shfl(l, 4 * g + i);
-                if (r < M) {
-                    const int t = w.q0 + r / p.gqa, h = hk * p.gqa + r % p.gqa;
+                if (r < HG * M) {
+                    const int rh = row_in_head(r);
+                    const int t = w.q0 + rh / p.gqa, h = (hk + row_head(r)) * p.gqa + rh % p.gqa;
                     const float inv = lr > 0.f ? 1.f / lr : 0.f;
                     float *op = p.out + ((int64_t) t * p.H + h) * D + DPL * n;
                     if constexpr (DPL % 4 == 0) {
@@ -264,7 +305,7 @@ __device__ __forceinline__ void decode_piece(const AttnParams &p, const SeqWindo
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int r = rt * 16 + 4 * g + i;
-                if (r < M) {
+                if (r < HG * M) {
                     float *op = LREC ? lrec + r * D + DPL * n : rec_o(p, pc.rec, 0, r, D) + DPL * n;
                     if constexpr (FUSED) {
 #pragma unroll
@@ -281,7 +322,7 @@ __device__ __forceinline__ void decode_piece(const AttnParams &p, const SeqWindo
                 }
             }
             const int r = rt * 16 + n;
-            if (g == 0 && r < M) {
+            if (g == 0 && r < HG * M) {
                 if constexpr (FUSED)
                     store_pair_agent(rec_ml(p, pc.rec, 0, r), m_run[rt], l);
                 else if constexpr (LREC)

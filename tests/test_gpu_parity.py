@@ -200,6 +200,10 @@ SMALL = {
     "d96_spec_verify_5": (32, 8, 96, [700, 101, 4101], [5, 5, 5], {}),
     "d96_swa_softcap": (16, 4, 96, [3000, 900], [1, 2], {"n_swa": 700, "softcap": 30.0}),
     "d96_random_positions_bs32": (8, 2, 96, [600, 300], [6, 3], {"pos_mode": "random", "bs": 32}),
+    # head pairs (two kv heads per wave): 8 rows per head fill the 16-row tile,
+    # long contexts split into 16-row records; an odd kv-head count keeps one head per wave
+    "d96_pairs_full_tile_splits": (32, 8, 96, [9000, 3000, 40], [2, 2, 2], {}),
+    "d96_odd_kv_heads": (12, 3, 96, [1500, 700], [1, 1], {}),
     # spec-verify launch (rows per kv head up to 32) holding sequences of 4 and 8 rows too
     "mixed_rows": (32, 8, 128, [600, 90, 1500], [1, 5, 2], {}),
     "q8_mixed_rows": (32, 8, 128, [600, 90, 1500], [1, 5, 2], {"k_type": Q8_0}),
