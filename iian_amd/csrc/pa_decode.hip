@@ -59,12 +59,16 @@ __global__ __launch_bounds__(256) void pa_merge_kernel(AttnParams p) {
     // (rows r of a group's segment: row r % M of its head r / M)
     const int s = blockIdx.x, hg = blockIdx.y;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int q0 = min(max(p.qsl[s], 0), p.T);
-    const int nq = min(max(p.qsl[s + 1], q0), p.T) - q0;
-    const int M = nq * p.gqa;
     const bool grouped = p.rec_heads > 1;
+    // the segment table entry and the query range in one round trip: the
+    // exit test below reads all three without short-circuit, so the entry is
+    // not loaded after a branch on the query count
     const int2 info = p.seg_info[grouped ? s : s * (p.Hkv / p.head_group) + hg];
-    if (nq <= 0 || M > p.decode_rows || info.y <= 1) return;
+    const int qa = p.qsl[s], qb = p.qsl[s + 1];
+    const int q0 = min(max(qa, 0), p.T);
+    const int nq = min(max(qb, q0), p.T) - q0;
+    const int M = nq * p.gqa;
+    if ((nq <= 0) | (M > p.decode_rows) | (info.y <= 1)) return;
     const int hr = grouped ? hg : 0;
     const int rec0 = info.x, ns = info.y;
     const bool dl_live = ALL || lane * DL < D;
