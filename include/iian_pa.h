@@ -316,7 +316,10 @@ int iian_pa_runtime_errors(iian_pa_runtime *rt, void *stream, int32_t *host_err)
  * MFMA attention kernels enter K as exactly these values (int8 q in f16, the
  * block scale d applied in fp32 after the product), but V as f16(q*d): q*d
  * rounded once to f16, as P is (pinned through attention outputs by
- * test_q8_attention_stages_v_as_f16_of_q_times_d).  A V value beyond the f16
+ * test_q8_attention_stages_v_as_f16_of_q_times_d).  The reference's own GPU
+ * path rounds dequantised Q8_0 K and V to f16 the same way before its flash
+ * attention (ggml_cast(get_rows(cache), F16), src/iian/graph.cpp:483-484),
+ * so f16(q*d) is what iian computes with on a GPU.  A V value beyond the f16
  * range (|q*d| > 65504, possible only when a block scale exceeds 65504/127 ~
  * 516) becomes +-inf there, and the outputs it reaches are not finite (inf,
  * or NaN where a masked cell's zero weight meets it), where the reference's
