@@ -175,6 +175,16 @@ SMALL = {
     # a batch with more row blocks than one round of slots (not split)
     "prefill_split_p0_d128": (32, 8, 128, [40, 300, 1000], [40, 300, 1], {}),
     "prefill_unsplit_many_rb_d64": (14, 2, 64, [700] * 8 + [900, 50], [600] * 8 + [1, 1], {}),
+    # ragged prefill batches (one chunk over a prefix several times longer than
+    # the others'): f16 (the mixed launch) and Q8_0, head size 64, a sliding
+    # window, positions that are not the engine's layout, a softcap with
+    # decode rows in the same launch
+    "prefill_split_ragged_d128": (32, 8, 128, [4000, 700, 900, 1200], [256, 256, 256, 256], {}),
+    "q8_prefill_split_ragged": (32, 8, 128, [4000, 700, 900, 1200], [256, 256, 256, 256], {"k_type": Q8_0}),
+    "prefill_split_ragged_d64": (14, 2, 64, [3000, 300], [200, 200], {}),
+    "prefill_split_swa": (32, 8, 128, [5000, 600], [256, 256], {"n_swa": 2000}),
+    "prefill_split_random_pos": (8, 2, 128, [3000, 200], [100, 100], {"pos_mode": "random"}),
+    "prefill_split_softcap_decode": (32, 8, 128, [3500, 800, 64], [128, 1, 1], {"softcap": 30.0}),
     # Q8_0 pools (decode / spec-verify kernel)
     "q8_decode_gqa4_d128": (32, 8, 128, [513, 77, 2048, 33], [1, 1, 1, 1], {"k_type": Q8_0}),
     "q8_spec_verify_5": (32, 8, 128, [700, 101, 4101], [5, 5, 5], {"k_type": Q8_0}),
