@@ -47,6 +47,7 @@ constexpr int kF16DecodeWavesPerCuPairs = 4;
 constexpr int kQ8DecodeWavesPerCu = 8;
 constexpr int kMaxWavesPerCu = kQ8DecodeWavesPerCu;
 constexpr int kDefaultCus = 256;   // an MI355X, when the device cannot be queried
+constexpr int kMaxHeadDim = 1024;  // largest head size the general kernel stages (pa_general.hip)
 constexpr int kMaxDevices = 64;
 
 // Compute units of device `dev`, queried once per device.
@@ -244,8 +245,11 @@ bool mfma_path(int type_k, int type_v, int head_dim, int head_dim_v, int bs_log2
            head_dim == head_dim_v && (head_dim == 64 || head_dim == 128 || head_dim == 256) && bs_log2 >= 3;
 }
 
+// Any head size the general kernel stages (1 .. 1024; the reference's op
+// takes any, paged_attn.cpp:96-100); a Q8_0 head slice is whole 32-value
+// blocks.
 bool head_size_ok(int type, int d) {
-    if (d < 4 || d > 512 || d % 4) return false;
+    if (d < 1 || d > kMaxHeadDim) return false;
     return type != IIAN_PA_TYPE_Q8_0 || d % 32 == 0;
 }
 
@@ -394,11 +398,13 @@ int run_attention(hipStream_t st, const float *q, const void *k_pool, const void
         int64_t ns = (8LL * cus + base - 1) / base;
         ns = std::min<int64_t>(ns, std::max<int64_t>(1, max_tiles / 2));
         ns = std::min<int64_t>(ns, 64);
-        const size_t per_split = (size_t) n_tokens * n_head * (size_t) (head_dim_v + 2) * sizeof(float) + 512;
+        // record rows are Dv rounded up to a multiple of 4 floats
+        const size_t dv4 = (size_t) (head_dim_v + 3) & ~(size_t) 3;
+        const size_t per_split = (size_t) n_tokens * n_head * (dv4 + 2) * sizeof(float) + 512;
         const size_t rec_cap = src.scratch ? std::min(wl.total, kScratchBytes) : wl.total;
         ns = std::min<int64_t>(ns, (int64_t) (rec_cap / per_split));
         g.n_split = (int) std::max<int64_t>(ns, 1);
-        const size_t o_bytes = align256((size_t) n_tokens * n_head * g.n_split * head_dim_v * sizeof(float));
+        const size_t o_bytes = align256((size_t) n_tokens * n_head * g.n_split * dv4 * sizeof(float));
         const size_t need = g.n_split > 1 ? o_bytes + (size_t) n_tokens * n_head * g.n_split * 2 * sizeof(float) : 0;
         const int rc = ws_resolve(src, st, need, &ws);
         if (rc) return rc;
@@ -638,6 +644,8 @@ int iian_pa_rope_kv_write(void *stream, const float *k_rows, const float *v_rows
     if (((uintptr_t) k_rows | (uintptr_t) v_rows | (uintptr_t) q_in | (uintptr_t) q_out | (uintptr_t) k_pool |
          (uintptr_t) v_pool) & 7)
         return IIAN_PA_ERR_ARG;
+    // pairs of values move as 8-byte accesses: rows of an odd head size are not 8-byte aligned
+    if ((head_dim | head_dim_v) & 1) return IIAN_PA_ERR_UNSUPPORTED;
     // a Q8_0 head row is quantised in its own 32-value blocks, staged whole (at most 512 values)
     if ((type_k == IIAN_PA_TYPE_Q8_0 && (head_dim % 32 || head_dim > 512)) ||
         (type_v == IIAN_PA_TYPE_Q8_0 && (head_dim_v % 32 || head_dim_v > 512)))

@@ -1,7 +1,11 @@
 // pa_general.hip - paged attention for every pool-type and head-size combination
 // the MFMA kernels are not built for: F32 pools, mixed K/V types (F32, F16,
-// Q8_0 in any pairing), head sizes 4 .. 512 in steps of 4 (Phi-3's 96, 80,
-// ...), Dv != D, and block sizes that are not a power of two >= 8.
+// Q8_0 in any pairing), any head size from 1 to 1024 (Phi-3's 96, 80, ...;
+// Q8_0 pools in multiples of 32), Dv != D, and block sizes that are not a
+// power of two >= 8.  Head sizes that are not multiples of 4 are staged in
+// LDS rows padded with zeros to the next multiple of 4 (the reference's
+// dot and axpy loops run to any D, paged_attn.cpp:39,50), with element-wise
+// global loads and stores, since their rows are not 16-byte aligned.
 //
 // The arithmetic is fp32 throughout, as in the reference's Kern<float> and
 // Kern<fp16> (src/iian/paged_attn.cpp:25-87): K and V are widened to fp32 when
@@ -47,22 +51,40 @@ constexpr int kGenWaves = 4;
 constexpr int kGenRowsPerWave = 4;
 constexpr int kGenRows = kGenWaves * kGenRowsPerWave;
 constexpr int kGenMaxTile = 32;
+constexpr int kGenOutChunks = 4;   // output quads per lane: Dv up to 4 * 64 * 4 = 1024
 
 // Raw bytes of 4 consecutive elements e .. e+3 (e % 4 == 0) of head slice
 // `head` of pool row `row`; zeros for row < 0 (a cell beyond the sequence,
 // which must stage as 0 so that P = 0 never meets a non-finite V).
+// elem: dim is not a multiple of 4, so the quad is loaded element by element
+// (the slice is not 16-byte aligned) and its elements at dim and beyond are 0.
 template <int TY>
 __device__ __forceinline__ u32x4 gen_load(const char *pool, int64_t row, int64_t row_bytes, int head, int dim,
-                                          int e) {
+                                          int e, bool elem) {
     u32x4 r = {0u, 0u, 0u, 0u};
     if (row < 0) return r;
     const char *base = pool + row * row_bytes;
     if constexpr (TY == 0) {
-        r = *(const u32x4 *) (base + ((int64_t) head * dim + e) * 4);
+        const uint32_t *src = (const uint32_t *) (base + ((int64_t) head * dim + e) * 4);
+        if (!elem) {
+            r = *(const u32x4 *) src;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; j++) r[j] = e + j < dim ? src[j] : 0u;
+        }
     } else if constexpr (TY == 1) {
-        const u32x2 x = *(const u32x2 *) (base + ((int64_t) head * dim + e) * 2);
-        r[0] = x[0];
-        r[1] = x[1];
+        const uint16_t *src = (const uint16_t *) (base + ((int64_t) head * dim + e) * 2);
+        if (!elem) {
+            const u32x2 x = *(const u32x2 *) src;
+            r[0] = x[0];
+            r[1] = x[1];
+        } else {
+            uint32_t h[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) h[j] = e + j < dim ? src[j] : 0u;
+            r[0] = h[0] | (h[1] << 16);
+            r[1] = h[2] | (h[3] << 16);
+        }
     } else {
         // Q8_0: block e/32 of the head slice is {f16 d, int8 q[32]} (ggml-common.h:251-256);
         // the 4 quants sit 2-byte aligned at 2 + e%32
@@ -102,22 +124,39 @@ __device__ __forceinline__ float gen_row_max(float v, int tc) {
     return v;
 }
 
+// An output quad at dst holding its row's elements e .. e+3, `left` of them
+// (from e) inside the row; elem: element by element (the row is not 16-byte
+// aligned), writing only those inside.
+__device__ __forceinline__ void gen_store(float *dst, int left, bool elem, const float4 &v) {
+    if (!elem) {
+        *(float4 *) dst = v;
+        return;
+    }
+    dst[0] = v.x;
+    if (left > 1) dst[1] = v.y;
+    if (left > 2) dst[2] = v.z;
+    if (left > 3) dst[3] = v.w;
+}
+
 }  // namespace
 
-// Dynamic LDS: K tile [TC][D+4] f32 | V tile [TC][Dv+4] f32 | q [16][D] f32 |
-// P [4 waves][TC][4 rows] f32.  The +4 pad spreads the cells of a QK^T read
-// over the banks.
+// Dynamic LDS: K tile [TC][D4+4] f32 | V tile [TC][Dv4+4] f32 | q [16][D4] f32 |
+// P [4 waves][TC][4 rows] f32, with D4, Dv4 the head sizes rounded up to a
+// multiple of 4 (the padding holds zeros).  The +4 pad spreads the cells of a
+// QK^T read over the banks.
 template <int KT, int VT>
 __global__ __launch_bounds__(kGenWaves * 64) void pa_general_kernel(GenParams p) {
     extern __shared__ __attribute__((aligned(16))) float gen_lds[];
     __shared__ int64_t rows_lds[2][kGenMaxTile];
 
     const int TC = p.tile_cells, D = p.D, Dv = p.Dv;
-    const int kst = D + 4, vst = Dv + 4;
+    const int D4 = (D + 3) & ~3, Dv4 = (Dv + 3) & ~3;
+    const bool kelem = (D & 3) != 0, velem = (Dv & 3) != 0;   // rows not 16-byte aligned: element-wise
+    const int kst = D4 + 4, vst = Dv4 + 4;
     float *Kl = gen_lds;
     float *Vl = Kl + TC * kst;
     float *Ql = Vl + TC * vst;
-    float *Pl = Ql + kGenRows * D;
+    float *Pl = Ql + kGenRows * D4;
 
     // workgroup -> (pair, row block, split); the splits of one row block are
     // neighbours, and so are the row blocks of one (sequence, kv head)
@@ -177,16 +216,22 @@ __global__ __launch_bounds__(kGenWaves * 64) void pa_general_kernel(GenParams p)
     const int t0 = min(nt, z * per), t1 = min(nt, t0 + per);
 
     // q rows of the workgroup into LDS (raw fp32; the scale follows the dot)
-    const int dq = D >> 2;
+    const int dq = D4 >> 2;
     for (int i = tid; i < kGenRows * dq; i += kGenWaves * 64) {
         const int r = i / dq, c4 = i - r * dq;
         const int rr = R0 + r;
         float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
         if (rr < M) {
             const int t = q0 + rr / p.gqa, h = hk * p.gqa + rr % p.gqa;
-            v = *(const float4 *) (p.q + ((int64_t) t * p.H + h) * D + 4 * c4);
+            const float *qp = p.q + ((int64_t) t * p.H + h) * D + 4 * c4;
+            if (!kelem) {
+                v = *(const float4 *) qp;
+            } else {
+                const int e = 4 * c4;
+                v = make_float4(qp[0], e + 1 < D ? qp[1] : 0.f, e + 2 < D ? qp[2] : 0.f, e + 3 < D ? qp[3] : 0.f);
+            }
         }
-        *(float4 *) (Ql + r * D + 4 * c4) = v;
+        *(float4 *) (Ql + r * D4 + 4 * c4) = v;
     }
 
     // pool rows of the TC cells of tile t (by threads 0 .. TC-1)
@@ -212,8 +257,8 @@ __global__ __launch_bounds__(kGenWaves * 64) void pa_general_kernel(GenParams p)
         }
     };
 
-    // per-thread quads of one tile: K quads i = tid + 256k of TC*D/4, V likewise
-    const int kq = TC * dq, vq = TC * (Dv >> 2);
+    // per-thread quads of one tile: K quads i = tid + 256k of TC*D4/4, V likewise
+    const int kq = TC * dq, vq = TC * (Dv4 >> 2);
     u32x4 kraw[4], vraw[4];
     auto load_tile = [&](int buf) {
 #pragma unroll
@@ -221,11 +266,11 @@ __global__ __launch_bounds__(kGenWaves * 64) void pa_general_kernel(GenParams p)
             const int i = tid + k * kGenWaves * 64;
             if (i < kq) {
                 const int c = i / dq, e = 4 * (i - c * dq);
-                kraw[k] = gen_load<KT>(p.k_pool, rows_lds[buf][c], p.k_row, hk, D, e);
+                kraw[k] = gen_load<KT>(p.k_pool, rows_lds[buf][c], p.k_row, hk, D, e, kelem);
             }
             if (i < vq) {
-                const int c = i / (Dv >> 2), e = 4 * (i - c * (Dv >> 2));
-                vraw[k] = gen_load<VT>(p.v_pool, rows_lds[buf][c], p.v_row, hk, Dv, e);
+                const int c = i / (Dv4 >> 2), e = 4 * (i - c * (Dv4 >> 2));
+                vraw[k] = gen_load<VT>(p.v_pool, rows_lds[buf][c], p.v_row, hk, Dv, e, velem);
             }
         }
     };
@@ -238,7 +283,7 @@ __global__ __launch_bounds__(kGenWaves * 64) void pa_general_kernel(GenParams p)
                 *(float4 *) (Kl + c * kst + e) = gen_widen<KT>(kraw[k]);
             }
             if (i < vq) {
-                const int c = i / (Dv >> 2), e = 4 * (i - c * (Dv >> 2));
+                const int c = i / (Dv4 >> 2), e = 4 * (i - c * (Dv4 >> 2));
                 *(float4 *) (Vl + c * vst + e) = gen_widen<VT>(vraw[k]);
             }
         }
@@ -246,14 +291,15 @@ __global__ __launch_bounds__(kGenWaves * 64) void pa_general_kernel(GenParams p)
 
     const int P = 64 / TC;                 // lanes per cell in QK^T
     const int cl = lane % TC, jl = lane / TC;
-    const int ndv = Dv >> 2;               // output quads per row
+    const int ndv = Dv4 >> 2;              // output quads per row
     float m_run[kGenRowsPerWave], l_run[kGenRowsPerWave];
-    float4 o[kGenRowsPerWave][2];
+    float4 o[kGenRowsPerWave][kGenOutChunks];
 #pragma unroll
     for (int i = 0; i < kGenRowsPerWave; i++) {
         m_run[i] = -INFINITY;
         l_run[i] = 0.f;
-        o[i][0] = o[i][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int k = 0; k < kGenOutChunks; k++) o[i][k] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
     float *Pw = Pl + wave * TC * 4;
 
@@ -265,12 +311,12 @@ __global__ __launch_bounds__(kGenWaves * 64) void pa_general_kernel(GenParams p)
         // scores of cell cl for the wave's rows
         float acc[kGenRowsPerWave] = {0.f, 0.f, 0.f, 0.f};
         const float *kr = Kl + cl * kst;
-        const float *qr = Ql + wave * kGenRowsPerWave * D;
-        for (int d = 4 * jl; d < D; d += 4 * P) {
+        const float *qr = Ql + wave * kGenRowsPerWave * D4;
+        for (int d = 4 * jl; d < D4; d += 4 * P) {
             const float4 k4 = *(const float4 *) (kr + d);
 #pragma unroll
             for (int i = 0; i < kGenRowsPerWave; i++) {
-                const float4 q4 = *(const float4 *) (qr + i * D + d);
+                const float4 q4 = *(const float4 *) (qr + i * D4 + d);
                 acc[i] = fmaf(q4.x, k4.x, acc[i]);
                 acc[i] = fmaf(q4.y, k4.y, acc[i]);
                 acc[i] = fmaf(q4.z, k4.z, acc[i]);
@@ -302,12 +348,16 @@ __global__ __launch_bounds__(kGenWaves * 64) void pa_general_kernel(GenParams p)
         if (jl == 0) *(float4 *) (Pw + 4 * cl) = make_float4(pv[0], pv[1], pv[2], pv[3]);
         lds_barrier<1>();   // this wave's P stores before its reads (no s_barrier)
 #pragma unroll
-        for (int i = 0; i < kGenRowsPerWave; i++) {
-            o[i][0].x *= alpha[i]; o[i][0].y *= alpha[i]; o[i][0].z *= alpha[i]; o[i][0].w *= alpha[i];
-            o[i][1].x *= alpha[i]; o[i][1].y *= alpha[i]; o[i][1].z *= alpha[i]; o[i][1].w *= alpha[i];
-        }
+        for (int i = 0; i < kGenRowsPerWave; i++)
 #pragma unroll
-        for (int k = 0; k < 2; k++) {
+            for (int k = 0; k < kGenOutChunks; k++) {
+                o[i][k].x *= alpha[i];
+                o[i][k].y *= alpha[i];
+                o[i][k].z *= alpha[i];
+                o[i][k].w *= alpha[i];
+            }
+#pragma unroll
+        for (int k = 0; k < kGenOutChunks; k++) {
             const int d4 = lane + 64 * k;
             if (d4 >= ndv) break;
             const float *vc = Vl + 4 * d4;
@@ -352,18 +402,19 @@ __global__ __launch_bounds__(kGenWaves * 64) void pa_general_kernel(GenParams p)
         if (p.n_split == 1) {
             const float inv = l_run[i] > 0.f ? 1.f / l_run[i] : 0.f;
 #pragma unroll
-            for (int k = 0; k < 2; k++) {
+            for (int k = 0; k < kGenOutChunks; k++) {
                 const int d4 = lane + 64 * k;
                 if (d4 < ndv)
-                    *(float4 *) (p.out + orow * Dv + 4 * d4) =
-                        make_float4(o[i][k].x * inv, o[i][k].y * inv, o[i][k].z * inv, o[i][k].w * inv);
+                    gen_store(p.out + orow * Dv + 4 * d4, Dv - 4 * d4, velem,
+                              make_float4(o[i][k].x * inv, o[i][k].y * inv, o[i][k].z * inv, o[i][k].w * inv));
             }
         } else {
+            // records are Dv4 floats a row, so every quad stays aligned
             const int64_t rec = orow * p.n_split + z;
 #pragma unroll
-            for (int k = 0; k < 2; k++) {
+            for (int k = 0; k < kGenOutChunks; k++) {
                 const int d4 = lane + 64 * k;
-                if (d4 < ndv) *(float4 *) (p.part_o + rec * Dv + 4 * d4) = o[i][k];
+                if (d4 < ndv) *(float4 *) (p.part_o + rec * Dv4 + 4 * d4) = o[i][k];
             }
             if (lane == 0) *(float2 *) (p.part_ml + 2 * rec) = make_float2(m_run[i], l_run[i]);
         }
@@ -394,8 +445,12 @@ __global__ __launch_bounds__(256) void pa_general_merge_kernel(GenParams p) {
     if (j < 0 || (j * p.gqa + h % p.gqa) >= p.n_rb * kGenRows) return;
     const float2 ml = lane < ns ? *(const float2 *) (p.part_ml + 2 * (row * ns + lane)) : make_float2(-INFINITY, 0.f);
     const float mx = wave_max(gen_row_max(ml.x, 16));
-    const int ndv = p.Dv >> 2;
-    float4 acc[2] = {make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f)};
+    const int Dv4 = (p.Dv + 3) & ~3;
+    const bool velem = (p.Dv & 3) != 0;
+    const int ndv = Dv4 >> 2;
+    float4 acc[kGenOutChunks];
+#pragma unroll
+    for (int k = 0; k < kGenOutChunks; k++) acc[k] = make_float4(0.f, 0.f, 0.f, 0.f);
     float lsum = 0.f;
     if (mx != -INFINITY) {
         const float w = ml.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml.x - mx);
@@ -404,9 +459,9 @@ __global__ __launch_bounds__(256) void pa_general_merge_kernel(GenParams p) {
         for (int r = 0; r < ns; r++) {
             const float wr = __shfl(w, r);
             if (wr == 0.f) continue;   // wave-uniform
-            const float *op = p.part_o + (row * ns + r) * p.Dv;
+            const float *op = p.part_o + (row * ns + r) * Dv4;
 #pragma unroll
-            for (int k = 0; k < 2; k++) {
+            for (int k = 0; k < kGenOutChunks; k++) {
                 const int d4 = lane + 64 * k;
                 if (d4 < ndv) {
                     const float4 v = *(const float4 *) (op + 4 * d4);
@@ -420,23 +475,26 @@ __global__ __launch_bounds__(256) void pa_general_merge_kernel(GenParams p) {
     }
     const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
 #pragma unroll
-    for (int k = 0; k < 2; k++) {
+    for (int k = 0; k < kGenOutChunks; k++) {
         const int d4 = lane + 64 * k;
         if (d4 < ndv)
-            *(float4 *) (p.out + row * p.Dv + 4 * d4) =
-                make_float4(acc[k].x * inv, acc[k].y * inv, acc[k].z * inv, acc[k].w * inv);
+            gen_store(p.out + row * p.Dv + 4 * d4, p.Dv - 4 * d4, velem,
+                      make_float4(acc[k].x * inv, acc[k].y * inv, acc[k].z * inv, acc[k].w * inv));
     }
 }
 
 size_t general_lds_bytes(int tile_cells, int D, int Dv) {
-    return ((size_t) tile_cells * (D + 4) + (size_t) tile_cells * (Dv + 4) + (size_t) kGenRows * D +
+    const size_t D4 = (size_t) (D + 3) & ~(size_t) 3, Dv4 = (size_t) (Dv + 3) & ~(size_t) 3;
+    return ((size_t) tile_cells * (D4 + 4) + (size_t) tile_cells * (Dv4 + 4) + (size_t) kGenRows * D4 +
             (size_t) kGenWaves * tile_cells * 4) *
            sizeof(float);
 }
 
+// Cells per tile: a tile's quads of each tensor stay within 4 per thread
+// (TC * D4 / 4 <= 1024), and its LDS below 100 KB at head size 1024.
 int general_tile_cells(int D, int Dv) {
     const int m = D > Dv ? D : Dv;
-    return m <= 128 ? 32 : (m <= 256 ? 16 : 8);
+    return m <= 128 ? 32 : (m <= 256 ? 16 : (m <= 512 ? 8 : 4));
 }
 
 int general_rows_per_block() { return kGenRows; }

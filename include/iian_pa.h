@@ -59,9 +59,9 @@ const char *iian_pa_status_string(int status);
  * ALiBi (max_alibi_bias == 0), K and V each F32, F16 or Q8_0 in any pairing
  * (the reference's four F16/F32 pairings, paged_attn.cpp:148-155, widened to
  * Q8_0), and head sizes head_dim (K) and head_dim_v (V, which may differ,
- * paged_attn.cpp:163) that are multiples of 4 in [4, 512], multiples of 32
- * for a Q8_0 pool.  The reference accepts any head size; sizes outside that
- * set are the documented remainder and return 0.
+ * paged_attn.cpp:163) from 1 to 1024, multiples of 32 for a Q8_0 pool.
+ * The reference accepts any head size (paged_attn.cpp:96-100); sizes above
+ * 1024 return 0.
  * Both f16 or both Q8_0 at head size 64, 128 or 256 with a power-of-two block
  * size >= 8 run on the MFMA kernels; every other accepted combination runs on
  * the general fp32 kernel (fp32 arithmetic throughout, F32 pools keep full
@@ -244,8 +244,9 @@ typedef struct {
  * differ in the last bit).  Conversions, slot rules and *err_flag bit 0 as
  * iian_pa_kv_write; q is rotated whatever the slot.  Rows, q and the pools
  * must be 8-byte aligned (IIAN_PA_ERR_ARG otherwise).  Returns
- * IIAN_PA_ERR_UNSUPPORTED for other rope modes, for n_dims above 512, and
- * for a Q8_0 pool whose head size is not a multiple of 32 or is above 512
+ * IIAN_PA_ERR_UNSUPPORTED for other rope modes, for n_dims above 512, for an
+ * odd head size, and for a Q8_0 pool whose head size is not a multiple of 32
+ * or is above 512
  * (each head's values are quantised in their own 32-value blocks, as
  * iian_pa_supported requires). */
 int iian_pa_rope_kv_write(void *stream, const float *k_rows, const float *v_rows, const float *q_in,

@@ -44,9 +44,8 @@ def test_status_strings(lib):
 def test_supported_matrix(lib):
     """iian_pa_supported accepts what paged_attn_supported accepts
     (paged_attn.cpp:15-18: K and V each F16 or F32, in any pairing, no ALiBi;
-    any head size, Dv from the V pool, :163), widened to Q8_0, within the
-    documented remainder: head sizes must be multiples of 4 in [4, 512]
-    (multiples of 32 for a Q8_0 pool)."""
+    any head size, Dv from the V pool, :163), widened to Q8_0: every head
+    size from 1 to 1024 (multiples of 32 for a Q8_0 pool)."""
     from iian_amd import paged_attn_supported as sup
     F32, F16, Q8 = 0, 1, 8
     for tk in (F32, F16, Q8):
@@ -55,12 +54,14 @@ def test_supported_matrix(lib):
                 assert sup(tk, tv, 0.0, d), (tk, tv, d)
                 assert sup(tk, tv, 0.0, d, 64) and sup(tk, tv, 0.0, 64, d)      # Dv != D
             assert not sup(tk, tv, 8.0, 128)                                   # ALiBi (paged_attn.cpp:17)
-    for d in (4, 8, 80, 100, 112, 200, 508):
+    for d in (1, 2, 3, 4, 6, 8, 50, 80, 100, 112, 130, 200, 508, 516, 1000, 1023):
         assert sup(F16, F16, 0.0, d) and sup(F32, F16, 0.0, d) and sup(F16, F32, 0.0, 64, d)
         assert not sup(Q8, F16, 0.0, d) and not sup(F16, Q8, 0.0, 64, d)      # Q8_0 rows: 32-element blocks
-    # the remainder: not a multiple of 4, or above 512
-    for d in (0, 2, 6, 50, 130, 516, 576, 1024):
-        assert not sup(F16, F16, 0.0, d) and not sup(F32, F32, 0.0, 64, d)
+    for d in (576, 1024):
+        assert sup(F16, F16, 0.0, d) and sup(Q8, Q8, 0.0, d) and sup(F32, F16, 0.0, 64, d)
+    # beyond what the general kernel stages
+    for d in (0, -4, 1025, 1056, 2048):
+        assert not sup(F16, F16, 0.0, d) and not sup(F32, F32, 0.0, 64, d) and not sup(Q8, Q8, 0.0, d)
     assert not sup(2, F16, 0.0, 128) and not sup(F16, 2, 0.0, 128)           # Q4_0 pools are not KV types here
 
 
@@ -99,8 +100,8 @@ def call_attention(lib, **over):
     ({"q": None}, -1), ({"k": None}, -1), ({"bt": None}, -1), ({"out": None}, -1), ({"pos": None}, -1),
     ({"H": 6, "Hkv": 4}, -2), ({"Hkv": 0}, -2), ({"T": -1}, -2), ({"maxq": 5}, -2), ({"num_blocks": 0}, -2),
     ({"n_swa": -1}, -2), ({"softcap": -1.0}, -2), ({"scale": float("nan")}, -2), ({"q": 0x1004}, -2),
-    ({"tk": 8, "tv": 8, "D": 80, "Dv": 80}, -3), ({"tk": 2, "tv": 2}, -3), ({"D": 130, "Dv": 130}, -3),
-    ({"D": 516, "Dv": 516}, -3), ({"Dv": 6}, -3), ({"bs": 0}, -2),
+    ({"tk": 8, "tv": 8, "D": 80, "Dv": 80}, -3), ({"tk": 2, "tv": 2}, -3), ({"D": 1028, "Dv": 1028}, -3),
+    ({"D": 2048, "Dv": 2048}, -3), ({"Dv": 1056}, -3), ({"D": 0, "Dv": 0}, -3), ({"bs": 0}, -2),
     ({"num_blocks": (1 << 28) + 1}, -3),                      # more than 2^32 cells on the MFMA path
     ({"tk": 0, "tv": 0, "max_blocks": 1 << 28}, -3),          # 2^32 cells in one sequence on the general path
     ({"ws": None}, -4), ({"ws_bytes": 16}, -4),
@@ -220,7 +221,7 @@ def test_noalloc_rejects_a_call_beyond_its_scratch(lib):
     # argument checks come first, as in iian_pa_attention
     assert f(None, None, 0x2000, 0x3000, 1, 1, 64, 0x4000, 4, 0x5000, 0x6000, 0x7000, 4, 2, 2, 8, 2, 128, 128, 16,
              0.1, 0.0, 1, 0, 0x8000, None) == _lib.ERR_NULL
-    assert f(None, 0x1000, 0x2000, 0x3000, 1, 1, 64, 0x4000, 4, 0x5000, 0x6000, 0x7000, 4, 2, 2, 8, 2, 130, 130, 16,
+    assert f(None, 0x1000, 0x2000, 0x3000, 1, 1, 64, 0x4000, 4, 0x5000, 0x6000, 0x7000, 4, 2, 2, 8, 2, 1028, 1028, 16,
              0.1, 0.0, 1, 0, 0x8000, None) == _lib.ERR_UNSUPPORTED
 
 
@@ -240,7 +241,7 @@ def test_runtime_rejects_invalid_configs(lib):
     assert create(max_seqs=0) == _lib.ERR_ARG
     assert create(n_head=30) == _lib.ERR_ARG            # not a multiple of n_head_kv
     assert create(block_size=0) == _lib.ERR_ARG
-    assert create(head_dim=130) == _lib.ERR_UNSUPPORTED
+    assert create(head_dim=1028) == _lib.ERR_UNSUPPORTED
     assert create(type_k=2) == _lib.ERR_UNSUPPORTED
     assert lib.iian_pa_runtime_create(None, None) == _lib.ERR_NULL
     lib.iian_pa_runtime_destroy(None)

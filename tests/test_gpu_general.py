@@ -58,6 +58,18 @@ GENERAL = {
     "f32_not_causal": (8, 2, 64, [300, 50], [20, 1], {"k_type": F32, "causal": False}),
     "f32_random_positions": (8, 2, 64, [300, 200], [6, 40], {"k_type": F32, "pos_mode": "random"}),
     "f32_long_splits": (8, 2, 128, [9000, 5000], [1, 1], {"k_type": F32}),
+    # head sizes that are not multiples of 4 (rows staged element-wise into
+    # zero-padded LDS rows) and above 512 (4-cell tiles, four output quads per
+    # lane), through both the single-range and the split-and-merge launches
+    "d70_f16_prefill": (8, 2, 70, [500, 90], [100, 1], {}),
+    "d3_f32_decode": (4, 2, 3, [300, 40], [1, 1], {"k_type": F32}),
+    "d130_dv33_f16": (8, 4, 130, [700, 200], [1, 40], {"Dv": 33}),
+    "d1_dv5_f32_splits": (4, 1, 1, [6000, 100], [1, 1], {"k_type": F32, "Dv": 5}),
+    "d576_dv512_f16_mla_like": (16, 1, 576, [900, 300], [1, 20], {"Dv": 512}),
+    "d1024_f32_splits": (4, 2, 1024, [3000, 80], [1, 2], {"k_type": F32}),
+    "d1000_f16_prefill": (4, 2, 1000, [400, 90], [70, 1], {}),
+    "q8_d1024": (4, 2, 1024, [600, 100], [1, 30], {"k_type": Q8_0}),
+    "d99_f16k_q8v_dv96": (8, 2, 99, [500, 300], [1, 12], {"v_type": Q8_0, "Dv": 96}),
     "f32_one_long_seq": (32, 8, 128, [32000], [1], {"k_type": F32}),
     "f32_prefix_shared": (32, 8, 128, [1200, 1100, 900, 300], [128, 64, 1, 1],
                           {"k_type": F32, "shared_blocks": 32, "shared_seqs": 3}),
