@@ -43,6 +43,8 @@ WORKLOADS = {
     "cfg5_global_prefill": "Gemma3-12B global layer, 256-token prefill chunk per seq, 32 seqs",
     "cfg5_local_prefill": "Gemma3-12B local layer (n_swa=1024), 256-token prefill chunk per seq, 32 seqs",
     "phi3_decode": "Phi-3.5-mini paged decode, H32/Hkv32/D96, 64 seqs, ctx log-uniform [512,8192], f16 KV",
+    "phi3_prefill": "Phi-3.5-mini chunked prefill, H32/Hkv32/D96, 4 chunks x 512 tokens over prior U[1024,4096], "
+                    "f16 KV",
 }
 
 
@@ -67,7 +69,7 @@ def launch_kernels(sp, pa, max_blocks: int, block_size: int, cus: int) -> str:
     rows = [int(n) * gqa for n in sp.n_q]
     if sp.D == 96 and sp.kv_type == pa.GGML_TYPE_F16 and max(rows) <= 32:
         return "pa_decode_f16_kernel<96> + pa_merge_kernel<96>"
-    if sp.D not in (64, 128, 256):
+    if sp.D not in (64, 96, 128, 256) or (sp.D == 96 and sp.kv_type != pa.GGML_TYPE_F16):
         return "pa_general_kernel + pa_general_merge_kernel"
     has_dec = any(0 < r <= 32 for r in rows)
     has_pf = any(r > 32 for r in rows)

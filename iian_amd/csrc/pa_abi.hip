@@ -238,8 +238,9 @@ int row_bytes(int type, int64_t elems, int64_t &out) {
 
 // The MFMA kernels: K and V both f16 or both Q8_0, head size 64, 128 or 256
 // for both, and a power-of-two block size of at least 8 (the 8-cell groups of
-// a tile must not straddle a block).  Everything else iian_pa_supported
-// accepts runs through the general fp32 kernel.
+// a tile must not straddle a block); f16 pools at head size 96 too (run_attention
+// checks those itself).  Everything else iian_pa_supported accepts runs
+// through the general fp32 kernel.
 bool mfma_path(int type_k, int type_v, int head_dim, int head_dim_v, int bs_log2) {
     return type_k == type_v && (type_k == IIAN_PA_TYPE_F16 || type_k == IIAN_PA_TYPE_Q8_0) &&
            head_dim == head_dim_v && (head_dim == 64 || head_dim == 128 || head_dim == 256) && bs_log2 >= 3;
@@ -348,12 +349,13 @@ int run_attention(hipStream_t st, const float *q, const void *k_pool, const void
     const int bs_log2 = log2_exact(block_size);
     const int gqa = n_head / n_head_kv;
 
-    // f16 pools at head size 96 (Phi-3) take the MFMA decode kernel when every
-    // sequence of the call is a decode or spec-verify row set; batches with
-    // prefill chunks take the general kernel
-    const bool decode96 = type_k == IIAN_PA_TYPE_F16 && type_v == IIAN_PA_TYPE_F16 && head_dim == 96 &&
-                          head_dim_v == 96 && bs_log2 >= 3 && (int64_t) max_query_len * gqa <= kDecodeRowsMax;
-    if (!mfma_path(type_k, type_v, head_dim, head_dim_v, bs_log2) && !decode96) {
+    // f16 pools at head size 96 (Phi-3) take the MFMA kernels too: the decode
+    // kernel when every sequence of the call is a decode or spec-verify row
+    // set, the mixed prefill launch otherwise
+    const bool f16_96 = type_k == IIAN_PA_TYPE_F16 && type_v == IIAN_PA_TYPE_F16 && head_dim == 96 &&
+                        head_dim_v == 96 && bs_log2 >= 3;
+    const bool decode96 = f16_96 && (int64_t) max_query_len * gqa <= kDecodeRowsMax;
+    if (!mfma_path(type_k, type_v, head_dim, head_dim_v, bs_log2) && !f16_96) {
         // General fp32 path.  Cell indices within a sequence and pool rows
         // are int32 / int64 there.
         if ((int64_t) max_blocks * block_size > INT32_MAX) return IIAN_PA_ERR_UNSUPPORTED;
@@ -490,7 +492,7 @@ int run_attention(hipStream_t st, const float *q, const void *k_pool, const void
             if (wtiles <= (int64_t) kSegSwaTilesPerWave * sw && (int64_t) n_seqs * n_head_kv >= cus) p.seg_waves = sw;
         }
     }
-    // Mixed batch over an f16 pool (head size 64 or 128): one launch holds the
+    // Mixed batch over an f16 pool (head size 64, 96 or 128): one launch holds the
     // prefill workgroups and, after them, the decode rows' stream-K workers,
     // which fill the CUs the MFMA-bound prefill leaves, and merge their split
     // segments themselves.

@@ -340,10 +340,15 @@ __device__ __forceinline__ void merge_tile16(const AttnParams &p, int rec0, int 
         const int t = q0 + r / p.gqa, h = hk * p.gqa + r % p.gqa;
         const float inv = ls[i] > 0.f ? 1.f / ls[i] : 0.f;
         float *op = p.out + ((int64_t) t * p.H + h) * D + DPL * n;
+        if constexpr (DPL % 4 == 0) {
 #pragma unroll
-        for (int d = 0; d < DPL; d += 4)
-            *(float4 *) (op + d) = make_float4(acc[i][d] * inv, acc[i][d + 1] * inv, acc[i][d + 2] * inv,
-                                               acc[i][d + 3] * inv);
+            for (int d = 0; d < DPL; d += 4)
+                *(float4 *) (op + d) = make_float4(acc[i][d] * inv, acc[i][d + 1] * inv, acc[i][d + 2] * inv,
+                                                   acc[i][d + 3] * inv);
+        } else {   // D = 96: 6 dims per lane, 8-byte aligned
+#pragma unroll
+            for (int d = 0; d < DPL; d += 2) *(float2 *) (op + d) = make_float2(acc[i][d] * inv, acc[i][d + 1] * inv);
+        }
     }
 }
 

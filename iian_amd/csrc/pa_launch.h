@@ -45,9 +45,9 @@ hipError_t launch_decode_q8(const AttnParams &p, int head_dim, hipStream_t strea
 hipError_t launch_merge(const AttnParams &p, int head_dim, hipStream_t stream);
 // MFMA prefill kernel (sequences with n_q*gqa > p.decode_rows); grid covers max_query_len*gqa rows.
 // Q8_0 pools at head size 64 and 128, and both pool types at 256 (f16 pools at
-// 64 and 128 take launch_mixed_f16).
+// 64, 96 and 128 take launch_mixed_f16).
 hipError_t launch_prefill(const AttnParams &p, int head_dim, int kv_type, int max_rows, hipStream_t stream);
-// A mixed batch over an f16 pool at head size 64 or 128 in one launch: prefill
+// A mixed batch over an f16 pool at head size 64, 96 or 128 in one launch: prefill
 // workgroups plus the decode rows' stream-K workers, which merge their split
 // segments themselves.
 hipError_t launch_mixed_f16(const AttnParams &p, int head_dim, int max_rows, hipStream_t stream);

@@ -30,7 +30,10 @@ struct PrefillShape {
     static constexpr int KK = D / 16;                          // QK^T k-steps (16 dims each)
     static constexpr int NO = D / 32;                          // PV output tiles (32 dims each)
     static constexpr int KSTRIDE = DMA ? D * 2 : D * 2 + 16;
-    static constexpr int VSTRIDE = DMA ? D * 2 : D * 2 + 64;
+    // (a V transpose read takes 64 bytes of each of 4 rows per 32 lanes, so
+    // register-staged rows sit 16 or 48 dwords apart: 192 bytes at D = 64 and
+    // 96, 320 at D = 128)
+    static constexpr int VSTRIDE = (DMA || D == 96) ? D * 2 : D * 2 + 64;
     static constexpr int KBYTES = PT * KSTRIDE;
     static constexpr int VBYTES = PT * VSTRIDE;
     static constexpr int CHUNKS = PT * (D / 8);                // 16-byte chunks per tile per tensor

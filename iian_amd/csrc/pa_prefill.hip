@@ -7,8 +7,8 @@
 // reuses each tile for its 32 rows.  f16 tiles at D >= 128 go straight from
 // HBM to LDS (global_load_lds_dwordx4, rows unpadded with their 16-byte chunks
 // XOR-swizzled, issued from inline asm so that reads of the other buffer do not
-// wait on them); D = 64 and Q8_0 tiles are staged through registers (padded
-// rows).  Per tile:
+// wait on them); D = 64 and 96 and Q8_0 tiles are staged through registers
+// (padded rows).  Per tile:
 //
 //   S^T = K * Q^T       v_mfma_f32_32x32x16_f16: K rows (cells) from LDS with
 //                       ds_read_b128 as the A operand, Q^T (f16 hi/lo pair)
@@ -572,6 +572,7 @@ static hipError_t launch_prefill_kv(const AttnParams &p, int head_dim, int max_r
 hipError_t launch_mixed_f16(const AttnParams &p, int head_dim, int max_rows, hipStream_t stream) {
     switch (head_dim) {
         case 64: return launch_prefill_t<64, 4, 1, true>(p, max_rows, stream);
+        case 96: return launch_prefill_t<96, 4, 1, true>(p, max_rows, stream);
         case 128: return launch_prefill_t<128, 4, 1, true>(p, max_rows, stream);
         default: return hipErrorInvalidValue;
     }
@@ -579,7 +580,7 @@ hipError_t launch_mixed_f16(const AttnParams &p, int head_dim, int max_rows, hip
 
 hipError_t launch_prefill(const AttnParams &p, int head_dim, int kv_type, int max_rows, hipStream_t stream) {
     if (head_dim == 256) return launch_prefill16(p, head_dim, kv_type, max_rows, stream);
-    // f16 pools at head size 64 and 128 take launch_mixed_f16, with or
+    // f16 pools at head size 64, 96 and 128 take launch_mixed_f16, with or
     // without decode rows
     return kv_type == 8 ? launch_prefill_kv<8>(p, head_dim, max_rows, stream) : hipErrorInvalidValue;
 }

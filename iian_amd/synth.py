@@ -18,8 +18,10 @@ Configurations (BASELINE.json ``configs``):
   cfg4            Llama-3-8B Q8_0 KV: 128 seqs, 4096 prior + 5 spec-verify queries
   cfg5_<l>_<k>    Gemma3-12B: H16/Hkv8/D256, 32 seqs, L~U[8192,32768]; l in
                   {local (n_swa=1024), global}; k in {decode, prefill (256-token chunk)}
-  phi3_decode     Phi-3.5-mini decode (head size 96, the general fp32 kernel):
-                  H32/Hkv32/D96, 64 seqs, L log-uniform [512,8192], f16 KV
+  phi3_decode     Phi-3.5-mini decode (head size 96): H32/Hkv32/D96, 64 seqs,
+                  L log-uniform [512,8192], f16 KV
+  phi3_prefill    Phi-3.5-mini chunked prefill: H32/Hkv32/D96, 4 chunks of 512 tokens
+                  over a prior context P~U[1024,4096], f16 KV
 """
 from __future__ import annotations
 
@@ -58,7 +60,7 @@ class Spec:
 def spec(name: str, seed: Optional[int] = None, small: bool = False) -> Spec:
     """The named configuration.  ``small`` shrinks sequence count and context
     (same heads, head size, formats and masks) for fast CPU-checked runs."""
-    base = {"cfg1": 1, "cfg2": 2, "cfg3": 3, "cfg3_prefill": 3, "cfg4": 4, "phi3_decode": 6}.get(name, 5)
+    base = {"cfg1": 1, "cfg2": 2, "cfg3": 3, "cfg3_prefill": 3, "cfg4": 4, "phi3_decode": 6, "phi3_prefill": 7}.get(name, 5)
     rng = np.random.default_rng(seed if seed is not None else base)
     sd = seed if seed is not None else base
     if name == "cfg1":
@@ -97,6 +99,12 @@ def spec(name: str, seed: Optional[int] = None, small: bool = False) -> Spec:
         L = np.exp(rng.uniform(math.log(512), math.log(hi), S)).astype(np.int64)
         nb = int(sum((l + 15) // 16 for l in L)) * 2
         return Spec(name, 32, 32, 96, L, np.ones(S, np.int64), nb, seed=sd)
+    if name == "phi3_prefill":
+        n_pre, chunk = (2, 64) if small else (4, 512)
+        p_lo, p_hi = (128, 256) if small else (1024, 4096)
+        L = rng.integers(p_lo, p_hi + 1, n_pre) + chunk
+        nb = int(sum((l + 15) // 16 for l in L)) * 2
+        return Spec(name, 32, 32, 96, L, np.full(n_pre, chunk, np.int64), nb, seed=sd)
     if name.startswith("cfg5"):
         _, layer, kind = name.split("_")
         S = 4 if small else 32

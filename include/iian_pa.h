@@ -62,10 +62,10 @@ const char *iian_pa_status_string(int status);
  * paged_attn.cpp:163) from 1 to 1024, multiples of 32 for a Q8_0 pool.
  * The reference accepts any head size (paged_attn.cpp:96-100); sizes above
  * 1024 return 0.
- * Both f16 or both Q8_0 at head size 64, 128 or 256 with a power-of-two block
- * size >= 8 run on the MFMA kernels; every other accepted combination runs on
- * the general fp32 kernel (fp32 arithmetic throughout, F32 pools keep full
- * precision). */
+ * Both f16 or both Q8_0 at head size 64, 128 or 256, and both f16 at head
+ * size 96, with a power-of-two block size >= 8 run on the MFMA kernels; every
+ * other accepted combination runs on the general fp32 kernel (fp32 arithmetic
+ * throughout, F32 pools keep full precision). */
 int iian_pa_supported(int type_k, int type_v, int head_dim, int head_dim_v, float max_alibi_bias);
 
 /* Replaces ggml_set_rows(cache, rows, slots) on the K or V pool

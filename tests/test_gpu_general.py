@@ -39,7 +39,9 @@ GENERAL = {
     "f16k_f32v_decode": (32, 8, 128, [700, 101, 4101], [1, 5, 1], {"k_type": F16, "v_type": F32}),
     "f32k_f16v_prefill": (8, 2, 128, [500, 90], [200, 1], {"k_type": F32, "v_type": F16}),
     "phi3_d96_decode_f32": (32, 32, 96, [800, 1200, 70], [1, 1, 1], {"k_type": F32}),   # f16 decode: MFMA kernel
-    "phi3_d96_prefill_gqa4": (40, 10, 96, [700, 300], [256, 33], {}),
+    # f16 prefill at head size 96 runs on the MFMA prefill kernel from 8-cell
+    # blocks up; 4-cell blocks keep this Phi-3 prefill on the general kernel
+    "phi3_d96_prefill_gqa4": (40, 10, 96, [700, 300], [256, 33], {"bs": 4}),
     "d80_f16_mixed": (16, 4, 80, [600, 64, 900], [100, 1, 1], {}),
     "d80_f32_decode": (8, 8, 80, [300, 1000], [1, 1], {"k_type": F32}),
     "dv64_d128_f16": (32, 8, 128, [600, 90, 1500], [1, 5, 200], {"Dv": 64}),

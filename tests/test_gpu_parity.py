@@ -214,6 +214,14 @@ SMALL = {
     # long contexts split into 16-row records; an odd kv-head count keeps one head per wave
     "d96_pairs_full_tile_splits": (32, 8, 96, [9000, 3000, 40], [2, 2, 2], {}),
     "d96_odd_kv_heads": (12, 3, 96, [1500, 700], [1, 1], {}),
+    # head size 96 f16 prefill on the MFMA prefill kernel (register-staged 64-cell
+    # tiles, 3 output tiles of 32 dims), alone and with decode rows in the same launch
+    "d96_prefill_gqa1": (32, 32, 96, [600, 200], [512, 70], {}),
+    "d96_mixed_prefill_decode": (32, 32, 96, [900, 1500, 700, 64], [256, 1, 1, 64], {}),
+    "d96_prefill_swa_softcap": (16, 4, 96, [2000, 1200], [256, 100], {"n_swa": 512, "softcap": 30.0}),
+    "d96_prefill_bs8_random_pos": (8, 2, 96, [700, 300], [200, 64], {"bs": 8, "pos_mode": "random"}),
+    "d96_prefill_ragged": (32, 8, 96, [3000, 300], [200, 200], {}),
+    "d96_prefill_not_causal": (8, 2, 96, [300, 50], [40, 1], {"causal": False}),
     # spec-verify launch (rows per kv head up to 32) holding sequences of 4 and 8 rows too
     "mixed_rows": (32, 8, 128, [600, 90, 1500], [1, 5, 2], {}),
     "q8_mixed_rows": (32, 8, 128, [600, 90, 1500], [1, 5, 2], {"k_type": Q8_0}),
