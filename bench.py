@@ -33,6 +33,8 @@ WORKLOADS = {
     "cfg1": "Qwen2.5-0.5B paged decode, H14/Hkv2/D64, 8 seqs, ctx U[64,1024], 1024-block f16 pool",
     "cfg2": "Llama-3-8B paged decode, H32/Hkv8/D128, 64 seqs, ctx log-uniform [512,8192], "
             "16-token f16 blocks in a 65536-block pool, + KV write of 64 tokens",
+    "cfg2_f32": "Llama-3-8B paged decode as cfg2 with F32 K/V pools (the general fp32 kernel), + KV write "
+                "of 64 tokens",
     "cfg3": "Qwen3-8B mixed batch, H32/Hkv8/D128: 4 prefill chunks x 512 over prior U[1024,4096] "
             "(1024-token shared prefix) + 32 decode tokens, f16 KV",
     "cfg3_prefill": "Qwen3-8B, H32/Hkv8/D128: the 4 prefill chunks of cfg3 alone (x 512 tokens over prior "
@@ -69,7 +71,8 @@ def launch_kernels(sp, pa, max_blocks: int, block_size: int, cus: int) -> str:
     rows = [int(n) * gqa for n in sp.n_q]
     if sp.D == 96 and sp.kv_type == pa.GGML_TYPE_F16 and max(rows) <= 32:
         return "pa_decode_f16_kernel<96> + pa_merge_kernel<96>"
-    if sp.D not in (64, 96, 128, 256) or (sp.D == 96 and sp.kv_type != pa.GGML_TYPE_F16):
+    if (sp.D not in (64, 96, 128, 256) or (sp.D == 96 and sp.kv_type != pa.GGML_TYPE_F16)
+            or sp.kv_type not in (pa.GGML_TYPE_F16, pa.GGML_TYPE_Q8_0)):
         return "pa_general_kernel + pa_general_merge_kernel"
     has_dec = any(0 < r <= 32 for r in rows)
     has_pf = any(r > 32 for r in rows)

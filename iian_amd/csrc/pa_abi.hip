@@ -387,17 +387,19 @@ int run_attention(hipStream_t st, const float *q, const void *k_pool, const void
         g.causal = causal ? 1 : 0;
         g.n_swa = n_swa;
         g.tile_cells = general_tile_cells(head_dim, head_dim_v);
-        const int rows = general_rows_per_block();
+        const int rows = general_rows_per_block((int) std::min<int64_t>((int64_t) max_query_len * gqa, INT32_MAX));
+        g.rows_per_block = rows;
         g.n_rb = (int) (((int64_t) max_query_len * gqa + rows - 1) / rows);
         // Split each row block's KV range until the launch holds about 8
-        // workgroups per CU, keeping at least 2 tiles per range of the
+        // workgroups per CU (16 for 4-row workgroups: cfg2's shape with F32
+        // pools ran 396 against 471 us), keeping at least 2 tiles per range of the
         // longest sequence the tables can hold, and the records inside the
         // workspace: [T*H][n_split] rows of (Dv floats) + (m, l).  The
         // no-allocation entry point's workspace is the scratch array, so its
         // records must also fit kScratchBytes (one range needs none).
         const int64_t base = (int64_t) n_seqs * n_head_kv * g.n_rb;
         const int64_t max_tiles = ((int64_t) max_blocks * block_size + g.tile_cells - 1) / g.tile_cells;
-        int64_t ns = (8LL * cus + base - 1) / base;
+        int64_t ns = ((rows == 4 ? 16LL : 8LL) * cus + base - 1) / base;
         ns = std::min<int64_t>(ns, std::max<int64_t>(1, max_tiles / 2));
         ns = std::min<int64_t>(ns, 64);
         // record rows are Dv rounded up to a multiple of 4 floats

@@ -15,9 +15,11 @@
 // as paged_attn.cpp:127, and P and V meet in fp32 FMAs.  F32 pools therefore
 // keep their full precision; nothing is narrowed to f16.
 //
-// Work split.  A workgroup of 4 waves owns 16 query rows of one (sequence,
-// kv head): rows r = j*gqa + g (query token j, head g of the GQA group), 4 per
-// wave, so the group shares every staged K/V tile.  It attends one of the
+// Work split.  A workgroup of 4 waves owns 4*RPW query rows of one (sequence,
+// kv head): rows r = j*gqa + g (query token j, head g of the GQA group), RPW
+// per wave (4, or 1 when no sequence has more than 4 rows per kv head, so
+// that decode calls keep all 4 waves busy), and the group shares every
+// staged K/V tile.  It attends one of the
 // row block's n_split equal ranges of TC-cell tiles (TC = 32, 16 or 8 as the
 // head sizes grow, so a tile stays near 16 KB per tensor).  With n_split = 1
 // the workgroup writes the normalised output rows; otherwise each range
@@ -26,9 +28,10 @@
 //
 // Per tile: the rows of its TC cells are looked up once through the block
 // table (any block size: cell = table[i / bs] * bs + i % bs,
-// include/iian/kv_cache.h:135-137); every thread loads its quads (4
-// consecutive elements) of the next tile into registers while the current
-// tile is computed from LDS, then widens them to fp32 into LDS.
+// include/iian/kv_cache.h:135-137), the table entries read two tiles ahead so
+// that no tile waits on them; every thread loads its quads (4 consecutive
+// elements) of the next tile into registers while the current tile is
+// computed from LDS, then widens them to fp32 into LDS.
 //
 //   S = Q K^T   lane (c, j) of a wave: cell c of the tile, dims 4j, 4j + 4P,
 //               ... (P = 64/TC lanes per cell), for the wave's 4 rows; the P
@@ -48,8 +51,7 @@ namespace iian_pa {
 namespace {
 
 constexpr int kGenWaves = 4;
-constexpr int kGenRowsPerWave = 4;
-constexpr int kGenRows = kGenWaves * kGenRowsPerWave;
+constexpr int kGenMaxRows = kGenWaves * 4;   // rows per workgroup at RPW = 4
 constexpr int kGenMaxTile = 32;
 constexpr int kGenOutChunks = 4;   // output quads per lane: Dv up to 4 * 64 * 4 = 1024
 
@@ -140,12 +142,16 @@ __device__ __forceinline__ void gen_store(float *dst, int left, bool elem, const
 
 }  // namespace
 
-// Dynamic LDS: K tile [TC][D4+4] f32 | V tile [TC][Dv4+4] f32 | q [16][D4] f32 |
-// P [4 waves][TC][4 rows] f32, with D4, Dv4 the head sizes rounded up to a
+// Dynamic LDS: K tile [TC][D4+4] f32 | V tile [TC][Dv4+4] f32 | q [4*RPW][D4] f32 |
+// P [4 waves][TC][RPW rows] f32, with D4, Dv4 the head sizes rounded up to a
 // multiple of 4 (the padding holds zeros).  The +4 pad spreads the cells of a
 // QK^T read over the banks.
-template <int KT, int VT>
-__global__ __launch_bounds__(kGenWaves * 64) void pa_general_kernel(GenParams p) {
+// RPW rows per wave.  At RPW = 1 (decode calls) the register allocator is
+// asked for three waves per SIMD: 168 VGPRs, three 4-wave workgroups per CU.
+template <int KT, int VT, int RPW>
+__global__ __launch_bounds__(kGenWaves * 64, RPW == 1 ? 3 : 1) void pa_general_kernel(GenParams p) {
+    constexpr int kGenRowsPerWave = RPW;
+    constexpr int kGenRows = kGenWaves * RPW;
     extern __shared__ __attribute__((aligned(16))) float gen_lds[];
     __shared__ int64_t rows_lds[2][kGenMaxTile];
 
@@ -234,24 +240,40 @@ __global__ __launch_bounds__(kGenWaves * 64) void pa_general_kernel(GenParams p)
         *(float4 *) (Ql + r * D4 + 4 * c4) = v;
     }
 
-    // pool rows of the TC cells of tile t (by threads 0 .. TC-1)
-    auto tile_rows = [&](int t, int buf) {
-        if (tid < TC) {
+    // pool rows of the TC cells of tile t (by threads 0 .. TC-1), in two
+    // steps: tile_bt issues the block-table read two tiles ahead (the entry
+    // stays in a register), tile_row turns it into the cell's pool row in LDS
+    // one tile later, so no tile waits on a table read
+    struct BtEntry {
+        int c, b;
+        int32_t id;
+    };
+    auto tile_bt = [&](int t) {
+        BtEntry e = {-1, 0, 0};
+        if (tid < TC && t < t1) {
             const int c = c_lo + t * TC + tid;
-            int64_t row = -1;
             if (c < c_hi) {
                 int b = c / p.block_size;
                 if (b >= p.max_blocks) {
                     if (p.err) atomicOr(p.err, 2);
                     b = p.max_blocks - 1;
                 }
-                int32_t id = p.bt[(int64_t) s * p.max_blocks + b];
+                e = {c, b, p.bt[(int64_t) s * p.max_blocks + b]};
+            }
+        }
+        return e;
+    };
+    auto tile_row = [&](const BtEntry &e, int buf) {
+        if (tid < TC) {
+            int64_t row = -1;
+            if (e.c >= 0) {
+                int32_t id = e.id;
                 if ((uint32_t) id >= (uint32_t) p.num_blocks) {
                     if (p.err) atomicOr(p.err, 2);
                     id = 0;
                 }
-                row = (int64_t) id * p.block_size + (c - b * p.block_size);
-                if (c - b * p.block_size >= p.block_size) row = (int64_t) id * p.block_size;   // clamped b
+                row = (int64_t) id * p.block_size + (e.c - e.b * p.block_size);
+                if (e.c - e.b * p.block_size >= p.block_size) row = (int64_t) id * p.block_size;   // clamped b
             }
             rows_lds[buf][tid] = row;
         }
@@ -301,7 +323,7 @@ __global__ __launch_bounds__(kGenWaves * 64) void pa_general_kernel(GenParams p)
 #pragma unroll
         for (int k = 0; k < kGenOutChunks; k++) o[i][k] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    float *Pw = Pl + wave * TC * 4;
+    float *Pw = Pl + wave * TC * RPW;
 
     auto compute = [&](int t) {
         const int base = c_lo + t * TC;
@@ -309,7 +331,7 @@ __global__ __launch_bounds__(kGenWaves * 64) void pa_general_kernel(GenParams p)
         if (p.causal && base > w_max) return;                          // after every row of the wave
         if (p.n_swa > 0 && base + TC - 1 <= w_min - p.n_swa) return;   // out of every row's window
         // scores of cell cl for the wave's rows
-        float acc[kGenRowsPerWave] = {0.f, 0.f, 0.f, 0.f};
+        float acc[kGenRowsPerWave] = {};
         const float *kr = Kl + cl * kst;
         const float *qr = Ql + wave * kGenRowsPerWave * D4;
         for (int d = 4 * jl; d < D4; d += 4 * P) {
@@ -345,7 +367,14 @@ __global__ __launch_bounds__(kGenWaves * 64) void pa_general_kernel(GenParams p)
             m_run[i] = mnew;
             l_run[i] = l_run[i] * alpha[i] + gen_row_sum(pv[i], TC);
         }
-        if (jl == 0) *(float4 *) (Pw + 4 * cl) = make_float4(pv[0], pv[1], pv[2], pv[3]);
+        if (jl == 0) {
+            if constexpr (RPW == 4) {
+                *(float4 *) (Pw + 4 * cl) = make_float4(pv[0], pv[1], pv[2], pv[3]);
+            } else {
+#pragma unroll
+                for (int i = 0; i < RPW; i++) Pw[RPW * cl + i] = pv[i];
+            }
+        }
         lds_barrier<1>();   // this wave's P stores before its reads (no s_barrier)
 #pragma unroll
         for (int i = 0; i < kGenRowsPerWave; i++)
@@ -363,8 +392,17 @@ __global__ __launch_bounds__(kGenWaves * 64) void pa_general_kernel(GenParams p)
             const float *vc = Vl + 4 * d4;
             for (int cc = 0; cc < TC; cc++) {
                 const float4 v4 = *(const float4 *) (vc + cc * vst);
-                const float4 pp = *(const float4 *) (Pw + 4 * cc);
-                const float pr[4] = {pp.x, pp.y, pp.z, pp.w};
+                float pr[RPW];
+                if constexpr (RPW == 4) {
+                    const float4 pp = *(const float4 *) (Pw + 4 * cc);
+                    pr[0] = pp.x;
+                    pr[1] = pp.y;
+                    pr[2] = pp.z;
+                    pr[3] = pp.w;
+                } else {
+#pragma unroll
+                    for (int i = 0; i < RPW; i++) pr[i] = Pw[RPW * cc + i];
+                }
 #pragma unroll
                 for (int i = 0; i < kGenRowsPerWave; i++) {
                     o[i][k].x = fmaf(pr[i], v4.x, o[i][k].x);
@@ -378,14 +416,16 @@ __global__ __launch_bounds__(kGenWaves * 64) void pa_general_kernel(GenParams p)
     };
 
     if (t0 < t1) {
-        tile_rows(t0, 0);
+        tile_row(tile_bt(t0), 0);
+        BtEntry next = tile_bt(t0 + 1);
         __syncthreads();
         load_tile(0);
         for (int t = t0; t < t1; t++) {
             const int buf = (t - t0) & 1;
             __syncthreads();   // every wave is done with the K/V tile in LDS
             store_tile();
-            if (t + 1 < t1) tile_rows(t + 1, buf ^ 1);
+            if (t + 1 < t1) tile_row(next, buf ^ 1);
+            next = tile_bt(t + 2);
             __syncthreads();
             if (t + 1 < t1) load_tile(buf ^ 1);
             compute(t);
@@ -442,7 +482,7 @@ __global__ __launch_bounds__(256) void pa_general_merge_kernel(GenParams p) {
         s = lo;
     }
     const int j = t - p.qsl[s];
-    if (j < 0 || (j * p.gqa + h % p.gqa) >= p.n_rb * kGenRows) return;
+    if (j < 0 || (j * p.gqa + h % p.gqa) >= p.n_rb * p.rows_per_block) return;
     const float2 ml = lane < ns ? *(const float2 *) (p.part_ml + 2 * (row * ns + lane)) : make_float2(-INFINITY, 0.f);
     const float mx = wave_max(gen_row_max(ml.x, 16));
     const int Dv4 = (p.Dv + 3) & ~3;
@@ -483,10 +523,10 @@ __global__ __launch_bounds__(256) void pa_general_merge_kernel(GenParams p) {
     }
 }
 
-size_t general_lds_bytes(int tile_cells, int D, int Dv) {
+size_t general_lds_bytes(int tile_cells, int D, int Dv, int rows_per_block) {
     const size_t D4 = (size_t) (D + 3) & ~(size_t) 3, Dv4 = (size_t) (Dv + 3) & ~(size_t) 3;
-    return ((size_t) tile_cells * (D4 + 4) + (size_t) tile_cells * (Dv4 + 4) + (size_t) kGenRows * D4 +
-            (size_t) kGenWaves * tile_cells * 4) *
+    return ((size_t) tile_cells * (D4 + 4) + (size_t) tile_cells * (Dv4 + 4) + (size_t) rows_per_block * D4 +
+            (size_t) tile_cells * rows_per_block) *
            sizeof(float);
 }
 
@@ -497,20 +537,28 @@ int general_tile_cells(int D, int Dv) {
     return m <= 128 ? 32 : (m <= 256 ? 16 : (m <= 512 ? 8 : 4));
 }
 
-int general_rows_per_block() { return kGenRows; }
+// Rows per workgroup: 4 (one per wave) when no sequence of the call has more
+// than 4 rows per kv head, else 16.
+int general_rows_per_block(int max_rows) { return max_rows <= kGenWaves ? kGenWaves : kGenMaxRows; }
 
-template <int KT, int VT>
-static hipError_t launch_general_t(const GenParams &p, hipStream_t stream) {
-    const size_t lds = general_lds_bytes(p.tile_cells, p.D, p.Dv);
+template <int KT, int VT, int RPW>
+static hipError_t launch_general_r(const GenParams &p, hipStream_t stream) {
+    const size_t lds = general_lds_bytes(p.tile_cells, p.D, p.Dv, kGenWaves * RPW);
     const int64_t nwg = (int64_t) p.S * p.Hkv * p.n_rb * p.n_split;
     if (nwg <= 0 || nwg > INT32_MAX) return hipErrorInvalidValue;
     if (lds > 64 * 1024) {   // head sizes above 256: more than 64 KB of dynamic LDS needs the opt-in
-        const hipError_t e = hipFuncSetAttribute((const void *) pa_general_kernel<KT, VT>,
+        const hipError_t e = hipFuncSetAttribute((const void *) pa_general_kernel<KT, VT, RPW>,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds);
         if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL((pa_general_kernel<KT, VT>), dim3((unsigned) nwg), dim3(kGenWaves * 64), lds, stream, p);
-    hipError_t e = hipGetLastError();
+    hipLaunchKernelGGL((pa_general_kernel<KT, VT, RPW>), dim3((unsigned) nwg), dim3(kGenWaves * 64), lds, stream, p);
+    return hipGetLastError();
+}
+
+template <int KT, int VT>
+static hipError_t launch_general_t(const GenParams &p, hipStream_t stream) {
+    hipError_t e = p.rows_per_block == kGenWaves ? launch_general_r<KT, VT, 1>(p, stream)
+                                                 : launch_general_r<KT, VT, 4>(p, stream);
     if (e != hipSuccess || p.n_split == 1) return e;
     const int64_t rows = (int64_t) p.T * p.H;
     hipLaunchKernelGGL(pa_general_merge_kernel, dim3((unsigned) ((rows + 3) / 4)), dim3(256), 0, stream, p);

@@ -22,7 +22,8 @@ struct GenParams {
     int32_t max_blocks, num_blocks, block_size;
     int32_t T, S, H, Hkv, gqa, D, Dv;
     int32_t max_q;              // the caller's max_query_len
-    int32_t n_rb;               // 16-row blocks launched per (sequence, kv head)
+    int32_t rows_per_block;     // query rows per workgroup: 4 or 16 (general_rows_per_block)
+    int32_t n_rb;               // row blocks launched per (sequence, kv head)
     int32_t n_split;            // KV ranges per row block (1 .. 64)
     int32_t tile_cells;         // TC: 32, 16 or 8
     float scale, softcap;
@@ -93,9 +94,9 @@ hipError_t launch_rope_kv_write(const RopeParams &p, int type_k, int type_v, hip
 // General fp32 path (pa_general.hip): any K/V types of F32, F16, Q8_0; head
 // sizes 4..512 in steps of 4; any block size.
 hipError_t launch_general(const GenParams &p, int type_k, int type_v, hipStream_t stream);
-size_t general_lds_bytes(int tile_cells, int D, int Dv);
+size_t general_lds_bytes(int tile_cells, int D, int Dv, int rows_per_block);
 int general_tile_cells(int D, int Dv);
-int general_rows_per_block();
+int general_rows_per_block(int max_rows);
 
 hipError_t launch_kv_write(const float *rows, int64_t n_rows, int64_t row_elems, const int64_t *slots, void *pool,
                            int64_t n_cells, int type, int32_t *err, hipStream_t stream);

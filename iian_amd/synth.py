@@ -11,6 +11,7 @@ Configurations (BASELINE.json ``configs``):
   cfg1            Qwen2.5-0.5B decode: H14/Hkv2/D64, 8 seqs, L~U[64,1024], 1024-block pool
   cfg2            Llama-3-8B decode: H32/Hkv8/D128, 64 seqs, L log-uniform [512,8192],
                   65536-block pool, plus the KV write of the 64 new tokens
+                  (cfg2_f32: the same with F32 K/V pools, the general fp32 kernel)
   cfg3            Qwen3-8B mixed batch: 4 prefill chunks of 512 tokens over a prior
                   context P~U[1024,4096] whose first 1024 tokens (64 blocks) are shared
                   by all 4 sequences, plus 32 decode tokens with L~U[1024,4096]
@@ -32,7 +33,8 @@ from typing import Dict, List, Optional
 import numpy as np
 import torch
 
-from .paged_attn import (GGML_TYPE_F16, GGML_TYPE_Q8_0, KVPool, PagedAttnParams, PagedBatch, set_rows)
+from .paged_attn import (GGML_TYPE_F16, GGML_TYPE_F32, GGML_TYPE_Q8_0, KVPool, PagedAttnParams, PagedBatch,
+                         set_rows)
 
 
 @dataclass
@@ -60,18 +62,20 @@ class Spec:
 def spec(name: str, seed: Optional[int] = None, small: bool = False) -> Spec:
     """The named configuration.  ``small`` shrinks sequence count and context
     (same heads, head size, formats and masks) for fast CPU-checked runs."""
-    base = {"cfg1": 1, "cfg2": 2, "cfg3": 3, "cfg3_prefill": 3, "cfg4": 4, "phi3_decode": 6, "phi3_prefill": 7}.get(name, 5)
+    base = {"cfg1": 1, "cfg2": 2, "cfg2_f32": 2, "cfg3": 3, "cfg3_prefill": 3, "cfg4": 4, "phi3_decode": 6,
+            "phi3_prefill": 7}.get(name, 5)
     rng = np.random.default_rng(seed if seed is not None else base)
     sd = seed if seed is not None else base
     if name == "cfg1":
         S = 8
         L = rng.integers(64, 1025, S)
         return Spec(name, 14, 2, 64, L, np.ones(S, np.int64), 1024, seed=sd)
-    if name == "cfg2":
+    if name in ("cfg2", "cfg2_f32"):
         S = 8 if small else 64
         hi = 1024 if small else 8192
         L = np.exp(rng.uniform(math.log(512), math.log(hi), S)).astype(np.int64)
-        return Spec(name, 32, 8, 128, L, np.ones(S, np.int64), 65536 if not small else 4096, seed=sd)
+        return Spec(name, 32, 8, 128, L, np.ones(S, np.int64), 65536 if not small else 4096,
+                    kv_type=GGML_TYPE_F32 if name == "cfg2_f32" else GGML_TYPE_F16, seed=sd)
     if name.startswith("cfg3"):
         n_pre, chunk, n_dec = (2, 64, 4) if small else (4, 512, 32)
         if name == "cfg3_prefill":  # the prefill chunks alone (the prefill kernel without the decode rows)
@@ -271,7 +275,7 @@ def algorithmic_bytes(w: Workload, include_kv_write: bool = True) -> int:
     (K and V), Q and O once, the block tables and per-token metadata, plus the
     KV write (f32 rows in, converted rows out, slots)."""
     sp = w.spec
-    e = 2.0 if sp.kv_type == GGML_TYPE_F16 else 34.0 / 32.0
+    e = {GGML_TYPE_F16: 2.0, GGML_TYPE_F32: 4.0}.get(sp.kv_type, 34.0 / 32.0)
     S = len(sp.seq_lens)
     kv = 0
     for s in range(S):
