@@ -38,8 +38,9 @@
 //               partial sums are added with xor shuffles
 //   softmax     online, exp2 domain, per row; masks as paged_attn.cpp:124
 //   O += P V    lane owns output dims 4l .. 4l+3 (and 256 + 4l ..) of the
-//               wave's 4 rows; P comes from LDS as one broadcast float4 per
-//               cell
+//               wave's rows; P comes from LDS as one broadcast float4 per
+//               cell (one float at RPW = 1).  At Dv <= 128 lanes l and l + 32
+//               own the same dims over the two halves of the tile's cells
 //
 // Semantics: paged_attn_impl (src/iian/paged_attn.cpp:90-146), all-masked rows
 // -> zeros (:132).
@@ -147,7 +148,9 @@ __device__ __forceinline__ void gen_store(float *dst, int left, bool elem, const
 // multiple of 4 (the padding holds zeros).  The +4 pad spreads the cells of a
 // QK^T read over the banks.
 // RPW rows per wave.  At RPW = 1 (decode calls) the register allocator is
-// asked for three waves per SIMD: 168 VGPRs, three 4-wave workgroups per CU.
+// asked for three waves per SIMD (at most 168 VGPRs): three 4-wave workgroups
+// per CU.  Four (128 VGPRs, 2 spilled) measured 1.5% faster at cfg2's shape
+// with F32 pools; left at three.
 template <int KT, int VT, int RPW>
 __global__ __launch_bounds__(kGenWaves * 64, RPW == 1 ? 3 : 1) void pa_general_kernel(GenParams p) {
     constexpr int kGenRowsPerWave = RPW;
@@ -314,6 +317,11 @@ __global__ __launch_bounds__(kGenWaves * 64, RPW == 1 ? 3 : 1) void pa_general_k
     const int P = 64 / TC;                 // lanes per cell in QK^T
     const int cl = lane % TC, jl = lane / TC;
     const int ndv = Dv4 >> 2;              // output quads per row
+    // Dv <= 128: a row's output quads fill half a wave, so the two lane halves
+    // take the two halves of the tile's cells in PV and add their sums at the end
+    const bool pv_halves = ndv <= 32;
+    const int pv_lane = pv_halves ? (lane & 31) : lane;
+    const int pv_c0 = pv_halves ? (lane >> 5) * (TC >> 1) : 0, pv_c1 = pv_halves ? pv_c0 + (TC >> 1) : TC;
     float m_run[kGenRowsPerWave], l_run[kGenRowsPerWave];
     float4 o[kGenRowsPerWave][kGenOutChunks];
 #pragma unroll
@@ -387,10 +395,10 @@ __global__ __launch_bounds__(kGenWaves * 64, RPW == 1 ? 3 : 1) void pa_general_k
             }
 #pragma unroll
         for (int k = 0; k < kGenOutChunks; k++) {
-            const int d4 = lane + 64 * k;
+            const int d4 = pv_lane + 64 * k;
             if (d4 >= ndv) break;
             const float *vc = Vl + 4 * d4;
-            for (int cc = 0; cc < TC; cc++) {
+            for (int cc = pv_c0; cc < pv_c1; cc++) {
                 const float4 v4 = *(const float4 *) (vc + cc * vst);
                 float pr[RPW];
                 if constexpr (RPW == 4) {
@@ -433,6 +441,15 @@ __global__ __launch_bounds__(kGenWaves * 64, RPW == 1 ? 3 : 1) void pa_general_k
     }
 
     if (!wave_live) return;
+    if (pv_halves) {   // lanes l and l + 32 hold the two cell halves' sums of the same quad
+#pragma unroll
+        for (int i = 0; i < kGenRowsPerWave; i++) {
+            o[i][0].x += __shfl_xor(o[i][0].x, 32);
+            o[i][0].y += __shfl_xor(o[i][0].y, 32);
+            o[i][0].z += __shfl_xor(o[i][0].z, 32);
+            o[i][0].w += __shfl_xor(o[i][0].w, 32);
+        }
+    }
 #pragma unroll
     for (int i = 0; i < kGenRowsPerWave; i++) {
         if (!rlive[i]) continue;
