@@ -324,6 +324,8 @@ def main() -> int:
         log(f"copy calibration: {n} bytes read, {n} bytes written")
 
     value = b_step / (ms_step * 1e-3) / 1e9
+    kernels = launch_kernels(sp, pa, int(w.batch.block_tables.shape[1]), w.batch.block_size,
+                             torch.cuda.get_device_properties(torch.cuda.current_device()).multi_processor_count)
     res = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -336,7 +338,8 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16",
+        # the arithmetic type: f16 MFMA operands (fp32 sums), or fp32 throughout on the general kernel
+        "dtype": "f32" if "general" in kernels else "f16",
         "data": "synthetic",
         "config": {
             "workload": f"{args.config}: " + WORKLOADS.get(args.config, args.config),
@@ -350,9 +353,7 @@ def main() -> int:
         "attn_tok_per_s": round(w.T / (attn_ms * 1e-3), 1),
         "roofline": {
             "bound": "mfma" if mfma_bound else "hbm",
-            "kernel": "iian_pa_attention (" + launch_kernels(
-                sp, pa, int(w.batch.block_tables.shape[1]), w.batch.block_size,
-                torch.cuda.get_device_properties(torch.cuda.current_device()).multi_processor_count) + ")",
+            "kernel": "iian_pa_attention (" + kernels + ")",
             "achieved": round(attn_tfs if mfma_bound else attn_gbs, 1),
             "peak": MFMA_F16_PEAK_TFLOPS if mfma_bound else HBM_PEAK_GBS,
             "unit": "TFLOP/s" if mfma_bound else "GB/s",
