@@ -34,7 +34,7 @@
 // computed from LDS, then widens them to fp32 into LDS.
 //
 //   S = Q K^T   lane (c, j) of a wave: cell c of the tile, dims 4j, 4j + 4P,
-//               ... (P = 64/TC lanes per cell), for the wave's 4 rows; the P
+//               ... (P = 64/TC lanes per cell), for the wave's rows; the P
 //               partial sums are added with xor shuffles
 //   softmax     online, exp2 domain, per row; masks as paged_attn.cpp:124
 //   O += P V    lane owns output dims 4l .. 4l+3 (and 256 + 4l ..) of the
