@@ -194,6 +194,11 @@ SMALL = {
     "q8_swa_d256": (16, 8, 256, [3000, 900], [1, 2], {"k_type": Q8_0, "n_swa": 1024}),
     "q8_long_splits": (8, 2, 128, [9000, 5000], [1, 1], {"k_type": Q8_0}),
     "q8_spec_one_long_seq": (32, 8, 128, [32000], [5], {"k_type": Q8_0}),   # 250 pieces x 2 row tiles
+    # spec-verify at head size 128 (two row tiles per kv head) with a window
+    # and softcap, and over an odd number of kv heads
+    "q8_spec_swa_softcap": (16, 4, 128, [3000, 130, 33], [5, 5, 4], {"k_type": Q8_0, "n_swa": 700,
+                                                                          "softcap": 30.0}),
+    "q8_spec_odd_kv_heads": (12, 3, 128, [900, 45], [5, 3], {"k_type": Q8_0}),
     "q8_block_size_32": (8, 2, 128, [500, 61], [1, 4], {"k_type": Q8_0, "bs": 32}),
     "q8_softcap": (8, 2, 128, [333, 77], [1, 3], {"k_type": Q8_0, "softcap": 30.0}),
     # Q8_0 pools through the prefill kernel
@@ -254,7 +259,7 @@ def staged_q8_v(v_row_bytes: np.ndarray, n_elems: int) -> np.ndarray:
         return (q * d).astype(np.float16).astype(np.float32).reshape(v_row_bytes.shape[0], n_elems)
 
 
-@pytest.mark.parametrize("kind", ["decode", "prefill"])
+@pytest.mark.parametrize("kind", ["decode", "spec", "prefill"])
 def test_q8_attention_stages_v_as_f16_of_q_times_d(pa, oracle, kind):
     """Pins the V values the Q8_0 attention kernels compute with: a query row
     that sees exactly one cell has softmax weight 1 on it, so its output is
@@ -264,9 +269,11 @@ def test_q8_attention_stages_v_as_f16_of_q_times_d(pa, oracle, kind):
     not finite (the staged value is +-inf, and the tile's masked cells, weight
     0, turn it into NaN), the documented limit of this staging."""
     banner(f"q8 staged V values, {kind}")
-    rng = np.random.default_rng(77 if kind == "decode" else 78)
+    rng = np.random.default_rng({"decode": 77, "spec": 79, "prefill": 78}[kind])
     H, Hkv, D = 32, 8, 128
-    lens, nq = ([1] * 48, [1] * 48) if kind == "decode" else ([160], [160])
+    # spec: 5-token verify batches (two row tiles per kv head); the first
+    # token of each sequence sees only cell 0
+    lens, nq = {"decode": ([1] * 48, [1] * 48), "spec": ([5] * 24, [5] * 24), "prefill": ([160], [160])}[kind]
     c = make_case(rng, H, Hkv, D, lens, nq, k_type=Q8_0, quantize=oracle.quantize_q8_0)
     n_cells = c.v_pool.shape[0]
     x = rng.standard_normal((n_cells, Hkv * D)).astype(np.float32)
@@ -280,7 +287,7 @@ def test_q8_attention_stages_v_as_f16_of_q_times_d(pa, oracle, kind):
     finite = np.ones((H, D), dtype=bool)
     finite[:gqa, 0] = False   # element 0 of kv head 0
     # each checked query row sees one cell: cell 0 of its sequence
-    for t in (range(c.T) if kind == "decode" else [0]):
+    for t in {"decode": range(c.T), "spec": range(0, c.T, 5), "prefill": [0]}[kind]:
         cell = int(c.bt[int(c.seq_idx[t]), 0]) * c.bs
         want = staged[cell].reshape(Hkv, D)[np.arange(H) // gqa]
         # exact equality as floats: the weighted sum over the tile's cells
