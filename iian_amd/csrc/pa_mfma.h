@@ -97,4 +97,39 @@ __device__ __forceinline__ f32x16 mfma32(const f16x8 &a, const f16x8 &b, const f
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
+// ---- The lo product of q in OCP E5M2 (bf8) ----
+//
+// An OCP E5M2 value is the top byte of the f16 encoding (sign, the same 5-bit
+// exponent with bias 15, the top 2 mantissa bits), so the f16 K rows in LDS
+// become bf8 operands with one v_perm per 4 values: rounded toward zero,
+// relative error below 2^-2.  The lo half of q (lo = x - f16(x), at most
+// 2^-11 |x|) only has to carry a few bits for the pair to hold q to ~2^-14;
+// it is stored as bf8(lo * 2^kLo8Shift), rounded to nearest even, and the
+// scaled MFMA applies 2^-kLo8Shift to it.  v_mfma_scale_f32_32x32x64_f8f6f4
+// takes 64 k values per lane pair at twice the issue time of one
+// v_mfma_f32_32x32x16_f16: the lo product of 64 dims costs 2 f16-MFMA slots
+// instead of 4.  Byte b of a lane's 32-byte operand (either side) carries the
+// same k index for A and B, so any consistent assignment of dims to bytes
+// computes the dot product.
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+constexpr int kLo8Shift = 12;
+
+__device__ __forceinline__ f32x16 mfma32_bf8_lo(const i32x8 &a, const i32x8 &b, const f32x16 &c) {
+    // A scale 2^0 (E8M0 127), B scale 2^-kLo8Shift
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 1, 1, 0, 127, 0, 127 - kLo8Shift);
+}
+
+// The top bytes (bf8, truncated) of the 4 f16 values in dwords lo, hi.
+__device__ __forceinline__ uint32_t f16x4_top_bytes(uint32_t lo, uint32_t hi) {
+    return __builtin_amdgcn_perm(hi, lo, 0x07050301u);
+}
+
+// bf8 of x, rounded to nearest even through f16, saturating at 57344.
+__device__ __forceinline__ uint32_t bf8_rne(float x) {
+    const uint32_t u = __builtin_bit_cast(uint16_t, (_Float16) x);
+    uint32_t m = u & 0x7fffu;
+    m = (m + 0x7fu + ((m >> 8) & 1u)) >> 8;
+    return ((u >> 8) & 0x80u) | min(m, 0x7bu);
+}
+
 }  // namespace iian_pa

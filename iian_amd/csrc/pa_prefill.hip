@@ -40,6 +40,10 @@
 #include "pa_mfma.h"
 #include "pa_decode_body.h"
 
+#ifndef IIAN_PA_PREFILL_LO8
+#define IIAN_PA_PREFILL_LO8 1
+#endif
+
 namespace iian_pa {
 
 // Waves per SIMD asked of the register allocator: two at D <= 128 (two 4-wave
@@ -83,6 +87,7 @@ __global__ __launch_bounds__(NW * 64, PrefillOcc<D>::kWavesPerSimd) void pa_pref
     constexpr int KK = SH::KK, NO = SH::NO, KSTRIDE = SH::KSTRIDE, VSTRIDE = SH::VSTRIDE;
     constexpr int PT = SH::PT, NH = SH::NH, NS = 16 * NH;   // cells per tile, 32-cell halves, scores per lane
     constexpr bool Q8 = KVT == 8;
+    constexpr bool LO8 = !Q8 && KK % 4 == 0 && IIAN_PA_PREFILL_LO8;   // lo product of q in bf8 (pa_mfma.h)
     constexpr int NT = NW * 64;
     constexpr int CPT = SH::CHUNKS / NT;          // f16: 16-byte chunks per thread per tensor
     static_assert(Q8 || CPT * NT == SH::CHUNKS, "tile chunks must divide evenly");
@@ -173,7 +178,11 @@ __global__ __launch_bounds__(NW * 64, PrefillOcc<D>::kWavesPerSimd) void pa_pref
     // Q^T B operands of query row n (pre-scaled f16 hi/lo pairs, dims
     // 16kk + 8hh .. +7), its position and running state.  The pair carries q
     // to ~2^-22 relative (split_f16x8).
-    f16x8 qv[KK], ql[KK];
+    // LO8 (f16 pools, KK a multiple of 4): the lo half as bf8 operands of the
+    // scaled fp8 MFMA, byte 8(kk%4) + e of ql8[kk/4] holding dim 16kk + 8hh + e
+    // (pa_mfma.h), where the K operand bytes of the same dims sit
+    f16x8 qv[KK], ql[LO8 ? 1 : KK];
+    i32x8 ql8[LO8 ? KK / 4 : 1];
     const int qr = Rw + n;
     int prow = wave_live ? w_max : 0;
     if (qr < M) {
@@ -181,12 +190,33 @@ __global__ __launch_bounds__(NW * 64, PrefillOcc<D>::kWavesPerSimd) void pa_pref
         prow = p.pos[t];
         const float *qp = p.q + ((int64_t) t * p.H + h) * D + 8 * hh;
 #pragma unroll
-        for (int kk = 0; kk < KK; kk++)
-            split_f16x8(*(const float4 *) (qp + 16 * kk), *(const float4 *) (qp + 16 * kk + 4), p.qscale, qv[kk],
-                        ql[kk]);
+        for (int kk = 0; kk < KK; kk++) {
+            if constexpr (LO8) {
+                const float4 xa = *(const float4 *) (qp + 16 * kk), xb = *(const float4 *) (qp + 16 * kk + 4);
+                const float x[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+                uint32_t w2[2] = {0u, 0u};
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const float xs = x[e] * p.qscale;
+                    float hv = (float) (_Float16) xs;
+                    asm volatile("" : "+v"(hv));
+                    qv[kk][e] = (_Float16) hv;
+                    w2[e >> 2] |= bf8_rne((xs - hv) * (float) (1 << kLo8Shift)) << (8 * (e & 3));
+                }
+                ql8[kk / 4][2 * (kk % 4)] = (int) w2[0];
+                ql8[kk / 4][2 * (kk % 4) + 1] = (int) w2[1];
+            } else {
+                split_f16x8(*(const float4 *) (qp + 16 * kk), *(const float4 *) (qp + 16 * kk + 4), p.qscale, qv[kk],
+                            ql[kk]);
+            }
+        }
     } else {
 #pragma unroll
-        for (int kk = 0; kk < KK; kk++) qv[kk] = ql[kk] = __builtin_bit_cast(f16x8, u32x4{0u, 0u, 0u, 0u});
+        for (int kk = 0; kk < KK; kk++) qv[kk] = __builtin_bit_cast(f16x8, u32x4{0u, 0u, 0u, 0u});
+#pragma unroll
+        for (int kk = 0; kk < (LO8 ? 1 : KK); kk++) ql[kk] = __builtin_bit_cast(f16x8, u32x4{0u, 0u, 0u, 0u});
+#pragma unroll
+        for (int b = 0; b < (LO8 ? KK / 4 : 1); b++) ql8[b] = i32x8{0, 0, 0, 0, 0, 0, 0, 0};
     }
     float m_run = -INFINITY, l_run = 0.f;   // of query row n (same in lanes n and n + 32)
     f32x16 o[NO];                           // O rows 8(r/4) + 4hh + r%4, dims 32m + n
@@ -386,23 +416,44 @@ __global__ __launch_bounds__(NW * 64, PrefillOcc<D>::kWavesPerSimd) void pa_pref
 #pragma unroll
             for (int kk = 0; kk < KK; kk++) ka[kk] = opaque(lds_addr(Kl + tile_off<D, DMA>(n, 32 * kk + 16 * hh, KSTRIDE)));
             __builtin_amdgcn_s_setprio(1);
+            if constexpr (LO8) {
+                // hi product per k-step in f16; the lo product per 4 k-steps
+                // in bf8, its K operand the top bytes of the same f16 reads
 #pragma unroll
-            for (int kk = 0; kk < KK; kk++)
+                for (int b = 0; b < KK / 4; b++) {
+                    i32x8 a8[NH];
 #pragma unroll
-                for (int c = 0; c < NH; c++) {
-                    const f16x8 a = lds_read_f16x8(ka[kk] + 32 * c * KSTRIDE);
-                    sa[c] = mfma32(a, qv[kk], sa[c]);
-                    sa[c] = mfma32(a, ql[kk], sa[c]);
+                    for (int j = 0; j < 4; j++)
+#pragma unroll
+                        for (int c = 0; c < NH; c++) {
+                            const f16x8 a = lds_read_f16x8(ka[4 * b + j] + 32 * c * KSTRIDE);
+                            sa[c] = mfma32(a, qv[4 * b + j], sa[c]);
+                            const u32x4 au = __builtin_bit_cast(u32x4, a);
+                            a8[c][2 * j] = (int) f16x4_top_bytes(au[0], au[1]);
+                            a8[c][2 * j + 1] = (int) f16x4_top_bytes(au[2], au[3]);
+                        }
+#pragma unroll
+                    for (int c = 0; c < NH; c++) sa[c] = mfma32_bf8_lo(a8[c], ql8[b], sa[c]);
                 }
-            // keep four K operand reads in flight ahead of the MFMAs instead of
-            // waiting on each read right before its MFMA
-            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+            } else {
 #pragma unroll
-            for (int j = 0; j < NH * KK - 4; j++) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                for (int kk = 0; kk < KK; kk++)
+#pragma unroll
+                    for (int c = 0; c < NH; c++) {
+                        const f16x8 a = lds_read_f16x8(ka[kk] + 32 * c * KSTRIDE);
+                        sa[c] = mfma32(a, qv[kk], sa[c]);
+                        sa[c] = mfma32(a, ql[kk], sa[c]);
+                    }
+                // keep four K operand reads in flight ahead of the MFMAs instead of
+                // waiting on each read right before its MFMA
+                __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+                for (int j = 0; j < NH * KK - 4; j++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+                __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
             }
-            __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
             __builtin_amdgcn_s_setprio(0);
         }
         float sv[NS];   // scores relative to mofs
