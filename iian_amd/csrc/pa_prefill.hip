@@ -87,7 +87,8 @@ __global__ __launch_bounds__(NW * 64, PrefillOcc<D>::kWavesPerSimd) void pa_pref
     constexpr int KK = SH::KK, NO = SH::NO, KSTRIDE = SH::KSTRIDE, VSTRIDE = SH::VSTRIDE;
     constexpr int PT = SH::PT, NH = SH::NH, NS = 16 * NH;   // cells per tile, 32-cell halves, scores per lane
     constexpr bool Q8 = KVT == 8;
-    constexpr bool LO8 = !Q8 && KK % 4 == 0 && IIAN_PA_PREFILL_LO8;   // lo product of q in bf8 (pa_mfma.h)
+    constexpr bool LO8 = !Q8 && IIAN_PA_PREFILL_LO8;   // lo product of q in bf8 (pa_mfma.h)
+    constexpr int NB8 = (KK + 3) / 4;                   // bf8 lo MFMAs per 32-cell half (the last one partial at D = 96)
     constexpr int NT = NW * 64;
     constexpr int CPT = SH::CHUNKS / NT;          // f16: 16-byte chunks per thread per tensor
     static_assert(Q8 || CPT * NT == SH::CHUNKS, "tile chunks must divide evenly");
@@ -178,11 +179,13 @@ __global__ __launch_bounds__(NW * 64, PrefillOcc<D>::kWavesPerSimd) void pa_pref
     // Q^T B operands of query row n (pre-scaled f16 hi/lo pairs, dims
     // 16kk + 8hh .. +7), its position and running state.  The pair carries q
     // to ~2^-22 relative (split_f16x8).
-    // LO8 (f16 pools, KK a multiple of 4): the lo half as bf8 operands of the
-    // scaled fp8 MFMA, byte 8(kk%4) + e of ql8[kk/4] holding dim 16kk + 8hh + e
-    // (pa_mfma.h), where the K operand bytes of the same dims sit
+    // LO8 (f16 pools): the lo half as bf8 operands of the scaled fp8 MFMA,
+    // byte 8(kk%4) + e of ql8[kk/4] holding dim 16kk + 8hh + e (pa_mfma.h),
+    // where the K operand bytes of the same dims sit; bytes past dim D are 0
     f16x8 qv[KK], ql[LO8 ? 1 : KK];
-    i32x8 ql8[LO8 ? KK / 4 : 1];
+    i32x8 ql8[LO8 ? NB8 : 1];
+#pragma unroll
+    for (int b = 0; b < (LO8 ? NB8 : 1); b++) ql8[b] = i32x8{0, 0, 0, 0, 0, 0, 0, 0};
     const int qr = Rw + n;
     int prow = wave_live ? w_max : 0;
     if (qr < M) {
@@ -215,8 +218,6 @@ __global__ __launch_bounds__(NW * 64, PrefillOcc<D>::kWavesPerSimd) void pa_pref
         for (int kk = 0; kk < KK; kk++) qv[kk] = __builtin_bit_cast(f16x8, u32x4{0u, 0u, 0u, 0u});
 #pragma unroll
         for (int kk = 0; kk < (LO8 ? 1 : KK); kk++) ql[kk] = __builtin_bit_cast(f16x8, u32x4{0u, 0u, 0u, 0u});
-#pragma unroll
-        for (int b = 0; b < (LO8 ? KK / 4 : 1); b++) ql8[b] = i32x8{0, 0, 0, 0, 0, 0, 0, 0};
     }
     float m_run = -INFINITY, l_run = 0.f;   // of query row n (same in lanes n and n + 32)
     f32x16 o[NO];                           // O rows 8(r/4) + 4hh + r%4, dims 32m + n
@@ -420,12 +421,16 @@ __global__ __launch_bounds__(NW * 64, PrefillOcc<D>::kWavesPerSimd) void pa_pref
                 // hi product per k-step in f16; the lo product per 4 k-steps
                 // in bf8, its K operand the top bytes of the same f16 reads
 #pragma unroll
-                for (int b = 0; b < KK / 4; b++) {
+                for (int b = 0; b < NB8; b++) {
                     i32x8 a8[NH];
 #pragma unroll
                     for (int j = 0; j < 4; j++)
 #pragma unroll
                         for (int c = 0; c < NH; c++) {
+                            if (4 * b + j >= KK) {   // past dim D (D = 96): zero bytes on both sides
+                                a8[c][2 * j] = a8[c][2 * j + 1] = 0;
+                                continue;
+                            }
                             const f16x8 a = lds_read_f16x8(ka[4 * b + j] + 32 * c * KSTRIDE);
                             sa[c] = mfma32(a, qv[4 * b + j], sa[c]);
                             const u32x4 au = __builtin_bit_cast(u32x4, a);

@@ -26,8 +26,17 @@
 // Semantics: paged_attn_impl (src/iian/paged_attn.cpp:90-146).
 #include "pa_common.h"
 #include "pa_launch.h"
+#include "pa_mfma.h"
 
 namespace iian_pa {
+
+// The lo product of q in bf8 (f16 pools; pa_mfma.h): one
+// v_mfma_scale_f32_16x16x128_f8f6f4 per 4 k-steps, at twice the issue time of
+// one v_mfma_f32_16x16x32_f16.  Lane (n, g) byte 8j + e of block b carries
+// dim 32(4b + j) + 8g + e on both sides.
+__device__ __forceinline__ f32x4 mfma16_bf8_lo(const i32x8 &a, const i32x8 &b, const f32x4 &c) {
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 1, 1, 0, 127, 0, 127 - kLo8Shift);
+}
 
 template <int D>
 struct PrefillShape16 {
@@ -67,6 +76,7 @@ __global__ __launch_bounds__(NW * 64, (D == 128 && KVT == 1) ? 4 : (D <= 128 ? 2
     using SH = PrefillShape16<D>;
     constexpr int KS = SH::KS, NPV = SH::NPV, KSTRIDE = SH::KSTRIDE, VSTRIDE = SH::VSTRIDE;
     constexpr bool Q8 = KVT == 8;
+    constexpr bool LO8 = !Q8 && KS % 4 == 0;      // lo product of q in bf8
     constexpr int CPT = SH::CHUNKS / (NW * 64);   // f16: 16-byte chunks per thread per tensor
     static_assert(Q8 || CPT * NW * 64 == SH::CHUNKS, "tile chunks must divide evenly");
     constexpr int NB = D / 32;                    // Q8_0 blocks per head slice
@@ -166,7 +176,10 @@ __global__ __launch_bounds__(NW * 64, (D == 128 && KVT == 1) ? 4 : (D <= 128 ? 2
 
     // Q^T B operands (pre-scaled f16 hi/lo pairs; measured: +4-6% time, the
     // score error of a single f16 q removed), row positions, running state
-    f16x8 qv[NRT][KS], ql[NRT][KS];
+    // (LO8: the lo half as bf8 operands, byte 8(ks%4) + e of ql8[rt][ks/4]
+    // holding dim 32ks + 8g + e)
+    f16x8 qv[NRT][KS], ql[NRT][LO8 ? 1 : KS];
+    i32x8 ql8[NRT][LO8 ? KS / 4 : 1];
     int prow[NRT];
     float m_run[NRT], l_run[NRT];
     f32x4 o[NRT][NPV];
@@ -179,13 +192,33 @@ __global__ __launch_bounds__(NW * 64, (D == 128 && KVT == 1) ? 4 : (D <= 128 ? 2
             prow[rt] = p.pos[t];
             const float *qp = p.q + ((int64_t) t * p.H + h) * D + 8 * g;
 #pragma unroll
-            for (int ks = 0; ks < KS; ks++)
-                split_f16x8(*(const float4 *) (qp + 32 * ks), *(const float4 *) (qp + 32 * ks + 4), p.qscale,
-                            qv[rt][ks], ql[rt][ks]);
+            for (int ks = 0; ks < KS; ks++) {
+                if constexpr (LO8) {
+                    const float4 xa = *(const float4 *) (qp + 32 * ks), xb = *(const float4 *) (qp + 32 * ks + 4);
+                    const float x[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+                    uint32_t w2[2] = {0u, 0u};
+#pragma unroll
+                    for (int e = 0; e < 8; e++) {
+                        const float xs = x[e] * p.qscale;
+                        float hv = (float) (_Float16) xs;
+                        asm volatile("" : "+v"(hv));
+                        qv[rt][ks][e] = (_Float16) hv;
+                        w2[e >> 2] |= bf8_rne((xs - hv) * (float) (1 << kLo8Shift)) << (8 * (e & 3));
+                    }
+                    ql8[rt][ks / 4][2 * (ks % 4)] = (int) w2[0];
+                    ql8[rt][ks / 4][2 * (ks % 4) + 1] = (int) w2[1];
+                } else {
+                    split_f16x8(*(const float4 *) (qp + 32 * ks), *(const float4 *) (qp + 32 * ks + 4), p.qscale,
+                                qv[rt][ks], ql[rt][ks]);
+                }
+            }
         } else {
 #pragma unroll
-            for (int ks = 0; ks < KS; ks++)
-                qv[rt][ks] = ql[rt][ks] = __builtin_bit_cast(f16x8, u32x4{0u, 0u, 0u, 0u});
+            for (int ks = 0; ks < KS; ks++) qv[rt][ks] = __builtin_bit_cast(f16x8, u32x4{0u, 0u, 0u, 0u});
+#pragma unroll
+            for (int ks = 0; ks < (LO8 ? 1 : KS); ks++) ql[rt][ks] = __builtin_bit_cast(f16x8, u32x4{0u, 0u, 0u, 0u});
+#pragma unroll
+            for (int b = 0; b < (LO8 ? KS / 4 : 1); b++) ql8[rt][b] = i32x8{0, 0, 0, 0, 0, 0, 0, 0};
         }
         m_run[rt] = -INFINITY;
         l_run[rt] = 0.f;
@@ -296,8 +329,23 @@ __global__ __launch_bounds__(NW * 64, (D == 128 && KVT == 1) ? 4 : (D <= 128 ? 2
 #pragma unroll
             for (int h = 0; h < 2; h++) {
                 f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+                if constexpr (LO8) {
 #pragma unroll
-                for (int ks = 0; ks < KS; ks++) {
+                    for (int b = 0; b < KS / 4; b++) {
+                        i32x8 a8;
+#pragma unroll
+                        for (int j = 0; j < 4; j++) {
+                            const int ks = 4 * b + j;
+                            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[h][ks], qv[rt][ks], acc, 0, 0, 0);
+                            const u32x4 au = __builtin_bit_cast(u32x4, ka[h][ks]);
+                            a8[2 * j] = (int) f16x4_top_bytes(au[0], au[1]);
+                            a8[2 * j + 1] = (int) f16x4_top_bytes(au[2], au[3]);
+                        }
+                        acc = mfma16_bf8_lo(a8, ql8[rt][b], acc);
+                    }
+                }
+#pragma unroll
+                for (int ks = 0; ks < (LO8 ? 0 : KS); ks++) {
                     if constexpr (Q8) {
                         // this lane's S^T rows are cells 8g + 4h + i; k-step ks = Q8_0 block ks
                         f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[h][ks], qv[rt][ks],
