@@ -8,6 +8,9 @@ library runs on, silently:
     hi/lo split of q (pa_common.h split_f16x8) was compiled to one and came out
     as hi - x instead of x - hi (caught by the peaked-score parity tests); the
     source keeps the compiler from forming it.
+It also checks that the prefill kernels' lo product of q runs on the scaled
+fp8 MFMA with both operands in bf8 (OCP E5M2, format code 1: cbsz:1 blgp:1),
+the format whose encoding is the top byte of an f16 (pa_mfma.h).
 """
 import re
 import shutil
@@ -44,3 +47,16 @@ def test_no_packed_fp32_and_no_negated_mixed_fma(tmp_path):
         assert not PACKED_F32.search(asm), (src, PACKED_F32.search(asm).group(0))
         m = NEG_MIX.search(asm)
         assert m is None, (src, m.group(0) if m else None)
+
+
+BF8_LO = re.compile(r"^\s*v_mfma_scale_f32_(32x32x64|16x16x128)_f8f6f4\s[^\n]*$", re.M)
+
+
+@pytest.mark.skipif(shutil.which("hipcc") is None and not Path("/opt/rocm/bin/hipcc").exists(),
+                    reason="hipcc not available")
+def test_prefill_lo_product_is_bf8(tmp_path):
+    for src, shape in (("pa_prefill.hip", "32x32x64"), ("pa_prefill16.hip", "16x16x128")):
+        lines = [m.group(0) for m in BF8_LO.finditer(device_asm(src, tmp_path))]
+        assert any(shape in l for l in lines), src
+        for l in lines:
+            assert "cbsz:1" in l and "blgp:1" in l, (src, l)
