@@ -420,25 +420,37 @@ __global__ __launch_bounds__(NW * 64, PrefillOcc<D>::kWavesPerSimd) void pa_pref
             if constexpr (LO8) {
                 // hi product per k-step in f16; the lo product per 4 k-steps
                 // in bf8, its K operand the top bytes of the same f16 reads
+                // K reads run AH reads ahead of their MFMA (rotating
+                // registers; scheduling fences keep the compiler from sinking
+                // each read next to its use, which left the read latency
+                // exposed on every k-step: cfg3_prefill 135.8 against 125.9 us
+                // with 4 ahead, 126.1-126.2 with 2 or 3; a workgroup alone on
+                // its CU, one wave per SIMD, has no other wave to hide it)
+                constexpr int NR = KK * NH, AH = 4;
+                auto rd = [&](int r) { return lds_read_f16x8(ka[r / NH] + 32 * (r % NH) * KSTRIDE); };
+                f16x8 ab[AH + 1];
 #pragma unroll
-                for (int b = 0; b < NB8; b++) {
-                    i32x8 a8[NH];
+                for (int r = 0; r < AH; r++) ab[r] = rd(r);
+                i32x8 a8[NH];
 #pragma unroll
-                    for (int j = 0; j < 4; j++)
+                for (int r = 0; r < NR; r++) {
+                    const int kk = r / NH, c = r % NH, j = kk % 4;
+                    if (r + AH < NR) ab[(r + AH) % (AH + 1)] = rd(r + AH);
+                    __builtin_amdgcn_sched_barrier(0);
+                    const f16x8 a = ab[r % (AH + 1)];
+                    sa[c] = mfma32(a, qv[kk], sa[c]);
+                    const u32x4 au = __builtin_bit_cast(u32x4, a);
+                    a8[c][2 * j] = (int) f16x4_top_bytes(au[0], au[1]);
+                    a8[c][2 * j + 1] = (int) f16x4_top_bytes(au[2], au[3]);
+                    if (kk == KK - 1 && (KK % 4) != 0) {   // D = 96: the last block's bytes past dim D are 0
 #pragma unroll
-                        for (int c = 0; c < NH; c++) {
-                            if (4 * b + j >= KK) {   // past dim D (D = 96): zero bytes on both sides
-                                a8[c][2 * j] = a8[c][2 * j + 1] = 0;
-                                continue;
-                            }
-                            const f16x8 a = lds_read_f16x8(ka[4 * b + j] + 32 * c * KSTRIDE);
-                            sa[c] = mfma32(a, qv[4 * b + j], sa[c]);
-                            const u32x4 au = __builtin_bit_cast(u32x4, a);
-                            a8[c][2 * j] = (int) f16x4_top_bytes(au[0], au[1]);
-                            a8[c][2 * j + 1] = (int) f16x4_top_bytes(au[2], au[3]);
-                        }
+                        for (int jj = KK % 4; jj < 4; jj++) a8[c][2 * jj] = a8[c][2 * jj + 1] = 0;
+                    }
+                    if (c == NH - 1 && (j == 3 || kk == KK - 1)) {
 #pragma unroll
-                    for (int c = 0; c < NH; c++) sa[c] = mfma32_bf8_lo(a8[c], ql8[b], sa[c]);
+                        for (int cc = 0; cc < NH; cc++) sa[cc] = mfma32_bf8_lo(a8[cc], ql8[kk / 4], sa[cc]);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
                 }
             } else {
 #pragma unroll
