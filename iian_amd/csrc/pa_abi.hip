@@ -430,7 +430,9 @@ int run_attention(hipStream_t st, const float *q, const void *k_pool, const void
     // The kernels index pool rows with 32-bit cell numbers and row lengths
     // (pool_off): 2^32 cells of the smallest supported row (68 bytes, one
     // Q8_0 head of size 64) are 272 GiB, more than an MI355X's 288 GB hold.
-    if (((int64_t) num_blocks << bs_log2) > ((int64_t) 1 << 32) || kr != vr || kr > (int64_t) UINT32_MAX)
+    // Rows stay below 1 GiB, so that a prefill DMA lane's byte offset within
+    // the 4 rows of its instruction fits 32 bits.
+    if (((int64_t) num_blocks << bs_log2) > ((int64_t) 1 << 32) || kr != vr || kr >= ((int64_t) 1 << 30))
         return IIAN_PA_ERR_UNSUPPORTED;
     p.k_row = kr;
     p.v_row = vr;

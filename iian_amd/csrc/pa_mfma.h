@@ -93,6 +93,12 @@ __device__ __forceinline__ void lds_load16(const void *gptr, uint32_t lds_off) {
     asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_off), "v"(gptr) : "m0");
 }
 
+// The same with a wave-uniform 64-bit base in SGPRs and the lane's 32-bit
+// byte offset (the saddr form): the per-instruction address work is scalar.
+__device__ __forceinline__ void lds_load16_s(const void *sbase, uint32_t voff, uint32_t lds_off) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds_off), "v"(voff), "s"(sbase) : "m0");
+}
+
 __device__ __forceinline__ f32x16 mfma32(const f16x8 &a, const f16x8 &b, const f32x16 &c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }

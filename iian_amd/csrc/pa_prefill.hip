@@ -282,6 +282,7 @@ __global__ __launch_bounds__(NW * 64, PrefillOcc<D>::kWavesPerSimd) void pa_pref
     const int64_t dma_lane_off =
         (int64_t) (lane / (2 * D / 16)) * p.k_row + head_off +
         16 * ((lane % (2 * D / 16)) ^ swz((RI * wave + lane / (2 * D / 16)) & 15));
+    const uint32_t dma_lane_off32 = (uint32_t) dma_lane_off;
     auto load_dma = [&](int tile, char *Kd, char *Vd) {
         if (((min(tile + PT - 1, L - 1) >> p.bs_log2) - tw.first) >= 64) table_load(p, s, tile >> p.bs_log2, L, tw);
         constexpr int NQ = SH::KBYTES / 1024 / NW;   // instructions per wave per tensor
@@ -291,11 +292,13 @@ __global__ __launch_bounds__(NW * 64, PrefillOcc<D>::kWavesPerSimd) void pa_pref
                 const int r0 = RI * (j * NW + wave);   // first row of this instruction
                 const int blk = __builtin_amdgcn_readlane(tw.id, ((tile + r0) >> p.bs_log2) - tw.first);
                 const uint32_t row = ((uint32_t) blk << p.bs_log2) | (uint32_t) ((tile + r0) & bs_mask);
-                const int64_t off = (int64_t) pool_off(row, p.k_row) + dma_lane_off;
                 const uint32_t lk = __builtin_amdgcn_readfirstlane((uint32_t) (uintptr_t) (Kd + (j * NW + wave) * 1024));
                 const uint32_t lv = __builtin_amdgcn_readfirstlane((uint32_t) (uintptr_t) (Vd + (j * NW + wave) * 1024));
-                lds_load16(p.k_pool + off, lk);
-                lds_load16(p.v_pool + off, lv);
+                // the rows' base in SGPRs, the lane's part a 32-bit offset
+                // (below 4 rows: the host admits rows shorter than 1 GiB)
+                const uint64_t rbase = pool_off(row, p.k_row);
+                lds_load16_s(p.k_pool + rbase, dma_lane_off32, lk);
+                lds_load16_s(p.v_pool + rbase, dma_lane_off32, lv);
             }
             return;
         }

@@ -116,7 +116,8 @@ size_t iian_pa_workspace_size(int32_t n_tokens, int32_t n_seqs, int32_t n_head, 
  * (paged_attn.cpp:132).
  *   q               f32 [T][H][D] (contiguous head vectors, paged_attn.cpp:161-162)
  *   k_pool, v_pool  the cell pools of one layer, num_blocks*block_size rows
- *                   (at most 2^32 rows: IIAN_PA_ERR_UNSUPPORTED beyond)
+ *                   (at most 2^32 rows, each under 1 GiB: IIAN_PA_ERR_UNSUPPORTED
+ *                   beyond)
  *   block_tables    int32 [S][max_blocks] physical block ids
  *   seq_lens        int32 [S] cells of each sequence, this step's included
  *                   (UBatch::SeqInfo::cells.size(), include/iian/graph.h:33-36)
