@@ -34,11 +34,12 @@ using namespace iian_pa;
 // against 824 us at 4 per CU).
 constexpr int kF16DecodeWavesPerCu = 6;
 // In the mixed prefill launch the decode workers' workgroups (4 waves each)
-// are dispatched first; at 2 waves per CU they take half the CUs' second
-// workgroup slot instead of every CU's (Qwen3-8B chunked prefill + 32 decode
-// rows: 176.6 against 181.3 us; with one chunk of no prior context 164.5
-// against 162.2 us; 1 per CU 205.6 us, 3 per CU 185.8 us).
-constexpr int kF16MixedDecodeWavesPerCu = 2;
+// are dispatched first and take a prefill workgroup's slot on their CU while
+// they run.  With the prefill kernel as it is now, 3 waves per CU (192
+// workgroups) measured best: Qwen3-8B chunked prefill + 32 decode rows 153.7
+// against 155.1 us at 2 per CU, 162.9 at 4, 204.9 at 1; with one chunk of no
+// prior context 147.6 against 157.1 at 2, 147.9 at 4, 208.4 at 1.
+constexpr int kF16MixedDecodeWavesPerCu = 3;
 constexpr int kF16DecodeWavesPerCuD256 = 3;
 // Head pairs at head size 96 (two kv heads per wave, twice the bytes per
 // unit of work): 4 waves per CU measured best at Phi-3.5 shapes (414 us
