@@ -62,10 +62,10 @@ struct PrefillOcc {
 //
 // MIXED: the launch of a mixed batch over an f16 pool.  The first n_dec
 // workgroups hold NW stream-K decode workers each (one wave per worker,
-// decode_piece of pa_decode_body.h) and are dispatched first, one per CU: the
-// HBM-bound decode waves and the MFMA-bound prefill workgroups then share
-// every CU from the start, instead of the decode rows waiting for the prefill
-// tail.  Split decode segments are merged inside the launch (arrive_last):
+// decode_piece of pa_decode_body.h) and are dispatched first, on three CUs in
+// four (kF16MixedDecodeWavesPerCu in pa_abi.hip): the HBM-bound decode waves
+// and the MFMA-bound prefill workgroups then share those CUs from the start,
+// instead of the decode rows waiting for the prefill tail.  Split decode segments are merged inside the launch (arrive_last):
 // the decode workers finish long before the prefill workgroups, so the merge
 // costs the launch nothing, and the call is one launch.
 template <int D, int NW, int KVT, bool MIXED>
