@@ -211,10 +211,28 @@ def main() -> int:
     def attention():
         attn_calls[cur[0]]()
 
-    def step():
+    def two_calls():
         kv_write()
         attention()
         cur[0] = (cur[0] + 1) % len(batches)
+
+    # f16 decode steps: the KV write and the attention in one launch
+    # (iian_pa_write_attention), where the library takes the call
+    fused_calls = [pa.bind_write_paged_attn(w.q, k_rows, v_rows, w.k_pool, w.v_pool, sp.Hkv, w.params, b, out=out,
+                                            workspace=ws) for b in batches]
+    try:
+        fused_calls[0]()
+        torch.cuda.synchronize()
+    except pa.PagedAttnError:
+        fused_calls = None
+
+    def fused():
+        fused_calls[cur[0]]()
+        cur[0] = (cur[0] + 1) % len(batches)
+
+    step = fused if fused_calls else two_calls
+    step_calls = ("iian_pa_write_attention (KV write and attention, one launch)" if fused_calls
+                  else "iian_pa_kv_write_kv + iian_pa_attention")
 
     # untimed warm-up: the W steps asked for, continued until 0.5 s have passed
     # so the GPU clocks have left their idle state before the timed region
@@ -236,7 +254,16 @@ def main() -> int:
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_step = wall * 1e3 / args.steps
-    log(f"timed {args.steps} steps: {ms_step * 1e3:.1f} us/step")
+    log(f"timed {args.steps} steps ({step_calls}): {ms_step * 1e3:.1f} us/step")
+    two_call_ms = None
+    if fused_calls:   # the same K steps as the two calls they replace
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            two_calls()
+        torch.cuda.synchronize()
+        two_call_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+        log(f"the same steps as two calls (kv write, attention): {two_call_ms * 1e3:.1f} us/step")
 
     # dominant launch: the attention call alone, HIP events on its stream.
     # First a pair around each call of K steps (the KV write between calls),
@@ -341,6 +368,8 @@ def main() -> int:
         # the arithmetic type: f16 MFMA operands (fp32 sums), or fp32 throughout on the general kernel
         "dtype": "f32" if "general" in kernels else "f16",
         "data": "synthetic",
+        "step_calls": step_calls,
+        "two_call_ms_per_step": round(two_call_ms, 5) if two_call_ms else None,
         "config": {
             "workload": f"{args.config}: " + WORKLOADS.get(args.config, args.config),
             "n_seqs": len(sp.seq_lens), "n_tokens": w.T, "sum_ctx": int(sp.seq_lens.sum()),

@@ -19,6 +19,7 @@ from .paged_attn import (  # noqa: F401
     bind_paged_attn,
     bind_rope_set_rows_kv,
     bind_set_rows_kv,
+    bind_write_paged_attn,
     build_batch,
     build_paged_attn,
     dequant_q8_0,
@@ -30,5 +31,6 @@ from .paged_attn import (  # noqa: F401
     set_rows_kv,
     swa_free_blocks,
     workspace_size,
+    write_paged_attn,
 )
 from ._lib import PagedAttnError  # noqa: F401

@@ -39,6 +39,9 @@ SIGNATURES = {
     "iian_pa_attention_noalloc": (C.c_int, [_P, _P, _P, _P, C.c_int, C.c_int, _I32, _P, _I32, _P, _P, _P,
                                             _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32,
                                             C.c_float, C.c_float, _I32, _I32, _P, _P]),
+    "iian_pa_write_attention": (C.c_int, [_P, _P, _P, _P, _P, _P, C.c_int, C.c_int, _I32, _P, _I32, _P, _P, _P,
+                                          _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32,
+                                          C.c_float, C.c_float, _I32, _I32, _P, _P, C.c_size_t, _P]),
     "iian_pa_build_batch": (C.c_int, [_P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P]),
     "iian_pa_swa_free_blocks": (C.c_int, [_P, _P, _P, _I32, _I32, _I32, _I32, _P, _P, _I32]),
     "iian_pa_rope_kv_write": (C.c_int, [_P, _P, _P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _I32, _P, _P, _P, _I64,

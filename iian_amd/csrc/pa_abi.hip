@@ -328,11 +328,15 @@ int run_attention(hipStream_t st, const float *q, const void *k_pool, const void
                   const int32_t *query_start_loc, const int32_t *pos, int32_t n_tokens, int32_t n_seqs,
                   int32_t max_query_len, int32_t n_head, int32_t n_head_kv, int32_t head_dim, int32_t head_dim_v,
                   int32_t block_size, float scale, float softcap, int32_t causal, int32_t n_swa, float *out,
-                  const WsSource &src, int32_t *err_flag) {
+                  const WsSource &src, int32_t *err_flag, const float *k_new = nullptr,
+                  const float *v_new = nullptr) {
     if (n_tokens < 0 || n_seqs < 0 || max_query_len < 0) return IIAN_PA_ERR_ARG;
     if (n_tokens == 0 || n_seqs == 0) return IIAN_PA_OK;
     if (!q || !k_pool || !v_pool || !block_tables || !seq_lens || !query_start_loc || !pos || !out)
         return IIAN_PA_ERR_NULL;
+    const bool write_new = k_new || v_new;   // iian_pa_write_attention
+    if (write_new && (!k_new || !v_new)) return IIAN_PA_ERR_NULL;
+    if (((uintptr_t) k_new | (uintptr_t) v_new) & 15) return IIAN_PA_ERR_ARG;
     if (n_head <= 0 || n_head_kv <= 0 || n_head % n_head_kv) return IIAN_PA_ERR_ARG;
     if (num_blocks <= 0 || max_blocks <= 0 || block_size <= 0 || max_query_len == 0 || max_query_len > n_tokens)
         return IIAN_PA_ERR_ARG;
@@ -356,6 +360,12 @@ int run_attention(hipStream_t st, const float *q, const void *k_pool, const void
     const bool f16_96 = type_k == IIAN_PA_TYPE_F16 && type_v == IIAN_PA_TYPE_F16 && head_dim == 96 &&
                         head_dim_v == 96 && bs_log2 >= 3;
     const bool decode96 = f16_96 && (int64_t) max_query_len * gqa <= kDecodeRowsMax;
+    // the fused KV write lives in the f16 decode kernels: f16 pools, one head
+    // size for K and V, every sequence of the call a decode or spec-verify row set
+    if (write_new && (type_k != IIAN_PA_TYPE_F16 || type_v != IIAN_PA_TYPE_F16 || head_dim != head_dim_v ||
+                      (int64_t) max_query_len * gqa > kDecodeRowsMax ||
+                      !(mfma_path(type_k, type_v, head_dim, head_dim_v, bs_log2) || f16_96)))
+        return IIAN_PA_ERR_UNSUPPORTED;
     if (!mfma_path(type_k, type_v, head_dim, head_dim_v, bs_log2) && !f16_96) {
         // General fp32 path.  Cell indices within a sequence and pool rows
         // are int32 / int64 there.
@@ -479,6 +489,9 @@ int run_attention(hipStream_t st, const float *q, const void *k_pool, const void
     p.rec_rows = p.decode_rows * p.head_group;
     p.rec_stride = (int64_t) p.rec_heads * p.rec_rows * head_dim_v + kRecordPad;
     const bool decode_only = max_rows <= p.decode_rows;
+    if (write_new && !decode_only) return IIAN_PA_ERR_UNSUPPORTED;
+    p.k_new = k_new;
+    p.v_new = v_new;
     // f16 decode calls with short or window-bounded segments: one workgroup
     // per (sequence, kv head) attends and merges in LDS, in one launch
     // (pa_decode_seg_kernel).  With no sliding window, when the block-table
@@ -581,6 +594,21 @@ int iian_pa_attention_noalloc(void *stream, const float *q, const void *k_pool, 
                          max_blocks, seq_lens, query_start_loc, pos, n_tokens, n_seqs, max_query_len, n_head,
                          n_head_kv, head_dim, head_dim_v, block_size, scale, softcap, causal, n_swa, out, src,
                          err_flag);
+}
+
+int iian_pa_write_attention(void *stream, const float *q, const float *k_new, const float *v_new, void *k_pool,
+                            void *v_pool, int type_k, int type_v, int32_t num_blocks, const int32_t *block_tables,
+                            int32_t max_blocks, const int32_t *seq_lens, const int32_t *query_start_loc,
+                            const int32_t *pos, int32_t n_tokens, int32_t n_seqs, int32_t max_query_len,
+                            int32_t n_head, int32_t n_head_kv, int32_t head_dim, int32_t head_dim_v,
+                            int32_t block_size, float scale, float softcap, int32_t causal, int32_t n_swa, float *out,
+                            void *workspace, size_t workspace_bytes, int32_t *err_flag) {
+    if (n_tokens > 0 && n_seqs > 0 && (!k_new || !v_new)) return IIAN_PA_ERR_NULL;
+    const WsSource src = {workspace, workspace_bytes, false};
+    return run_attention((hipStream_t) stream, q, k_pool, v_pool, type_k, type_v, num_blocks, block_tables,
+                         max_blocks, seq_lens, query_start_loc, pos, n_tokens, n_seqs, max_query_len, n_head,
+                         n_head_kv, head_dim, head_dim_v, block_size, scale, softcap, causal, n_swa, out, src,
+                         err_flag, k_new, v_new);
 }
 
 int iian_pa_build_batch(void *stream, const int32_t *block_ids, const int32_t *block_off,

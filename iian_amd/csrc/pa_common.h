@@ -36,6 +36,8 @@ struct AttnParams {
     int2 *seg_info;             // per segment: (first record, pieces), written by the segment's first piece
     uint64_t *seg_ctr;          // per (sequence, kv head): (call epoch << 16) | pieces counted in (mixed launch)
     int32_t *err;               // nullable error word
+    const float *k_new;         // iian_pa_write_attention: the step's new K rows, f32 [T][Hkv*D] (else null)
+    const float *v_new;         // and V rows, f32 [T][Hkv*Dv]
     int64_t k_row;              // bytes per K pool row (< 2^32)
     int64_t v_row;              // equal to k_row: K and V share type and head size
     int64_t rec_stride;         // floats per record of part_o

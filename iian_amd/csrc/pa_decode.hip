@@ -38,10 +38,11 @@ namespace iian_pa {
 // 1.5 waves per SIMD are launched at D <= 128 (kF16DecodeWaves in pa_abi.hip),
 // within a register budget of two waves per SIMD up to D*NRT = 128 (a budget
 // of one wave per SIMD measured slower).
-template <int D, int NRT, int HG = 1>
+// WR: iian_pa_write_attention (the pieces write the step's new K/V rows).
+template <int D, int NRT, int HG = 1, bool WR = false>
 __global__ __launch_bounds__(64, (D * NRT <= 128) ? 2 : 1) void pa_decode_f16_kernel(AttnParams p) {
     for_each_piece<false>(p, blockIdx.x, 0, [&](const SeqWindow &w, const Piece &pc) {
-        decode_piece<D, NRT, false, false, HG>(p, w, pc);
+        decode_piece<D, NRT, false, false, HG, WR>(p, w, pc);
     });
 }
 
@@ -172,7 +173,7 @@ hipError_t launch_merge(const AttnParams &p, int head_dim, hipStream_t stream) {
 // Gemma3-12B's sliding-window layer (256 segments of 1024-cell windows, D =
 // 256) the call takes 54.4-54.6 us here against 56.8-58.8 us (4 waves per
 // segment; 3 waves measured the same, 2 waves 58.5 us).
-template <int D, int NW>
+template <int D, int NW, bool WR = false>
 __global__ __launch_bounds__(64 * NW) void pa_decode_seg_kernel(AttnParams p) {
     __shared__ __attribute__((aligned(16))) float lrec[NW][16 * D + 32];
     const int s = blockIdx.x / p.Hkv, hk = blockIdx.x - s * p.Hkv;
@@ -251,7 +252,7 @@ __global__ __launch_bounds__(64 * NW) void pa_decode_seg_kernel(AttnParams p) {
         const int c1 = min(cb + kTile - 1, w.L - 1);
         if ((cb >> p.bs_log2) < tw.first || (c1 >> p.bs_log2) - tw.first >= 64)
             table_load(p, s, cb >> p.bs_log2, w.L, tw);
-        decode_piece<D, 1, false, true>(p, w, pc, &lrec[wave][0], &tw);
+        decode_piece<D, 1, false, true, 1, WR>(p, w, pc, &lrec[wave][0], &tw);
     }
     if (pc.pieces == 1) return;   // the one piece wrote the output
     __syncthreads();
@@ -283,9 +284,17 @@ __global__ __launch_bounds__(64 * NW) void pa_decode_seg_kernel(AttnParams p) {
 
 template <int D, int NRT, int HG = 1>
 static hipError_t launch_decode_t(const AttnParams &p, hipStream_t stream) {
-    hipLaunchKernelGGL((pa_decode_f16_kernel<D, NRT, HG>), dim3(p.sk_workers), dim3(64), 0, stream, p);
+    const dim3 grid(p.sk_workers);
+    if (p.k_new) hipLaunchKernelGGL((pa_decode_f16_kernel<D, NRT, HG, true>), grid, dim3(64), 0, stream, p);
+    else hipLaunchKernelGGL((pa_decode_f16_kernel<D, NRT, HG>), grid, dim3(64), 0, stream, p);
     const hipError_t e = hipGetLastError();
     return e != hipSuccess ? e : launch_merge(p, D, stream);
+}
+
+template <int D, int NW>
+static void launch_seg(const AttnParams &p, dim3 grid, hipStream_t stream) {
+    if (p.k_new) hipLaunchKernelGGL((pa_decode_seg_kernel<D, NW, true>), grid, dim3(64 * NW), 0, stream, p);
+    else hipLaunchKernelGGL((pa_decode_seg_kernel<D, NW>), grid, dim3(64 * NW), 0, stream, p);
 }
 
 hipError_t launch_decode(const AttnParams &p, int head_dim, int kv_type, hipStream_t stream) {
@@ -296,16 +305,10 @@ hipError_t launch_decode(const AttnParams &p, int head_dim, int kv_type, hipStre
     if (p.seg_waves > 0) {
         if (nrt != 1) return hipErrorInvalidValue;
         const dim3 grid((unsigned) ((int64_t) p.S * p.Hkv));
-        if (head_dim == 64 && p.seg_waves == kSegWavesD64)
-            hipLaunchKernelGGL((pa_decode_seg_kernel<64, kSegWavesD64>), grid, dim3(64 * kSegWavesD64), 0, stream, p);
-        else if (head_dim == 128 && p.seg_waves == kSegWavesD128)
-            hipLaunchKernelGGL((pa_decode_seg_kernel<128, kSegWavesD128>), grid, dim3(64 * kSegWavesD128), 0, stream,
-                               p);
-        else if (head_dim == 256 && p.seg_waves == kSegWavesD256)
-            hipLaunchKernelGGL((pa_decode_seg_kernel<256, kSegWavesD256>), grid, dim3(64 * kSegWavesD256), 0, stream,
-                               p);
-        else
-            return hipErrorInvalidValue;
+        if (head_dim == 64 && p.seg_waves == kSegWavesD64) launch_seg<64, kSegWavesD64>(p, grid, stream);
+        else if (head_dim == 128 && p.seg_waves == kSegWavesD128) launch_seg<128, kSegWavesD128>(p, grid, stream);
+        else if (head_dim == 256 && p.seg_waves == kSegWavesD256) launch_seg<256, kSegWavesD256>(p, grid, stream);
+        else return hipErrorInvalidValue;
         return hipGetLastError();
     }
     switch (head_dim) {

@@ -86,6 +86,46 @@ __device__ __forceinline__ void load_v(const AttnParams &p, const TableWindow &t
     }
 }
 
+// iian_pa_write_attention: the query tokens of a decode sequence are the
+// step's new tokens, and token t's K/V rows belong at the cell of its position
+// pos[t] (the slot the engine's set_rows writes).  The piece whose tile range
+// [cb, ce) holds that cell writes f16(row) (RNE, as iian_pa_kv_write
+// converts) for its kv heads at the start of the piece: each (cell, kv head)
+// slice lies in exactly one piece of its segment, so every new row is written
+// once.  The tile loop waits for the stores (vmcnt(0)) before it loads a tile
+// that holds a query position, so this wave reads the new rows back from its
+// own XCD's L2; no other segment reads those bytes.  One 16-byte chunk of one
+// row per lane and step.
+// The row comes from the block table itself (the piece's table window need
+// not reach the cell); a row whose block id lies outside the pool is not
+// written (bit 0, as iian_pa_kv_write flags a slot it skips).
+template <int D, int HG>
+__device__ __forceinline__ void write_new_rows(const AttnParams &p, const SeqWindow &w, int s, int cb, int ce,
+                                               int hk0) {
+    constexpr int CH = D / 8;   // 16-byte chunks per head slice
+    const int lane = threadIdx.x & 63;
+    const int64_t rk = (int64_t) p.Hkv * D;   // f32 row elements of k_new and v_new
+    for (int j = 0; j < w.nq; j++) {
+        const int t = w.q0 + j;
+        const int ps = p.pos[t];
+        if (ps < cb || ps >= ce || ps >= w.L) continue;   // wave-uniform
+        const int b = ps >> p.bs_log2;
+        const int32_t id = b < p.max_blocks ? p.bt[(int64_t) s * p.max_blocks + b] : -1;
+        if ((uint32_t) id >= (uint32_t) p.num_blocks) {
+            if (lane == 0 && p.err) atomicOr(p.err, 1);
+            continue;
+        }
+        const uint32_t row = ((uint32_t) id << p.bs_log2) | (uint32_t) (ps & ((1 << p.bs_log2) - 1));
+        for (int it = lane; it < 2 * HG * CH; it += 64) {
+            const int tv = it / (HG * CH), hk = hk0 + (it / CH) % HG, c = it % CH;
+            const float *src = (tv ? p.v_new : p.k_new) + (int64_t) t * rk + hk * D + 8 * c;
+            const float4 a = *(const float4 *) src, b = *(const float4 *) (src + 4);
+            const u32x4 v = {pack_f16x2(a.x, a.y), pack_f16x2(a.z, a.w), pack_f16x2(b.x, b.y), pack_f16x2(b.z, b.w)};
+            *(u32x4 *) ((char *) (tv ? p.v_pool : p.k_pool) + pool_off(row, p.k_row) + (hk * D * 2 + 16 * c)) = v;
+        }
+    }
+}
+
 // One piece: window tiles [pc.t0, pc.t1) of sequence pc.s at kv head pc.hk.
 // FUSED: a split segment is merged by its last piece to finish (arrive_last),
 // not by pa_merge_kernel.  LREC (NRT = 1, pa_decode_seg_kernel): the block-
@@ -99,7 +139,7 @@ __device__ __forceinline__ void load_v(const AttnParams &p, const TableWindow &t
 // tile is row r % M of head r / M (M <= 8 rows per head); QK^T and PV run once
 // per head, each on the other head's rows too, and each lane keeps the head
 // of its own row.
-template <int D, int NRT, bool FUSED = false, bool LREC = false, int HG = 1>
+template <int D, int NRT, bool FUSED = false, bool LREC = false, int HG = 1, bool WR = false>
 __device__ __forceinline__ void decode_piece(const AttnParams &p, const SeqWindow &w, const Piece &pc,
                                              float *lrec = nullptr, const TableWindow *tw_pre = nullptr) {
     static_assert(!LREC || (NRT == 1 && !FUSED), "LDS records hold one 16-row tile");
@@ -150,13 +190,33 @@ __device__ __forceinline__ void decode_piece(const AttnParams &p, const SeqWindo
     }
 
     const bool own1 = HG > 1 && row_head(n) == 1;   // this lane's row (column of S^T, row of P) is of head slot 1
+    // iian_pa_write_attention: this piece's new rows first; a tile that holds a
+    // query position is loaded only after the stores completed
+    constexpr bool wr = WR;   // p.k_new is set
+    auto new_cells = [&](int t0) { return wr && t0 <= w.pmax && t0 + kTile > w.pmin; };
+    // (when the first tile holds none, its loads go out before the rows are
+    // read and stored, so that round trip overlaps the tile's)
+    const bool first_new = cb < ce && new_cells(cb);
+    if constexpr (WR) {
+        if (first_new) write_new_rows<D, HG>(p, w, s, cb, ce, hk);
+        // a new token whose position is not a cell of its sequence is not
+        // written either (bit 0); the segment's first piece at kv head 0 says so
+        if (pc.t0 == 0 && hk == 0 && p.err)
+            for (int j = 0; j < w.nq; j++) {
+                const int ps = p.pos[w.q0 + j];
+                if ((ps < 0 || ps >= w.L) && lane == 0) atomicOr(p.err, 1);
+            }
+    }
     if (cb < ce) {
+        if (first_new) __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0)
         KRegs<D> kr[HG];
         VRegs<D> vr[HG];
 #pragma unroll
         for (int i = 0; i < HG; i++) load_k<D, NT>(p, tw, w.L, hk + i, cb, kr[i]);
 #pragma unroll
         for (int i = 0; i < HG; i++) load_v<D, NT>(p, tw, w.L, hk + i, cb, vr[i]);
+        if constexpr (WR)
+            if (!first_new) write_new_rows<D, HG>(p, w, s, cb, ce, hk);
         for (int tile = cb; tile < ce; tile += kTile) {
             const int next = tile + kTile;
             const bool has_next = next < ce;
@@ -187,6 +247,7 @@ __device__ __forceinline__ void decode_piece(const AttnParams &p, const SeqWindo
                         for (int e = 0; e < 4; e++) sacc[rt][h][e] = own1 ? acc[HG - 1][e] : acc[0][e];
                     }
                 }
+            if (has_next && new_cells(next)) __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): the new rows are stored
             if (has_next)
 #pragma unroll
                 for (int i = 0; i < HG; i++) load_k<D, NT>(p, tw, w.L, hk + i, next, kr[i]);

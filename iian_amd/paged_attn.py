@@ -606,6 +606,52 @@ def bind_paged_attn(q: torch.Tensor, k_cache: KVPool, v_cache: KVPool, n_head_kv
     return call
 
 
+def _write_attn_args(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, k_cache: KVPool, v_cache: KVPool,
+                     n_head_kv: int, params: PagedAttnParams, batch: PagedBatch, out: Optional[torch.Tensor],
+                     workspace: Optional[torch.Tensor], err_flag: Optional[torch.Tensor]):
+    """Checks a call of iian_pa_write_attention and returns (out, its argument tuple)."""
+    out, args = _attn_call(q, k_cache, v_cache, n_head_kv, params, batch, out, workspace, err_flag)
+    T, _, D = q.shape
+    for name, t, pool in (("k_new", k_new, k_cache), ("v_new", v_new, v_cache)):
+        if t.dtype != torch.float32 or not t.is_contiguous() or t.device != q.device:
+            raise ValueError(f"{name} must be a contiguous f32 tensor on q's device")
+        if t.numel() != T * pool.n_embd or (t.dim() >= 1 and t.shape[0] != T):
+            raise ValueError(f"{name} must hold one pool row of f32 per token: [{T}, {pool.n_embd}]")
+    return out, args[:2] + (k_new.data_ptr(), v_new.data_ptr()) + args[2:]
+
+
+def write_paged_attn(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, k_cache: KVPool, v_cache: KVPool,
+                     n_head_kv: int, params: PagedAttnParams, batch: PagedBatch, out: Optional[torch.Tensor] = None,
+                     workspace: Optional[torch.Tensor] = None,
+                     err_flag: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The layer's set_rows of the new K/V rows at their positions' cells
+    (src/iian/graph.cpp:319-320) and its paged attention
+    (graph.cpp:331-336) in one launch, for f16 decode and spec-verify steps
+    (iian_pa_write_attention); raises PagedAttnError (IIAN_PA_ERR_UNSUPPORTED)
+    for other calls, which take set_rows_kv and build_paged_attn."""
+    out, args = _write_attn_args(q, k_new, v_new, k_cache, v_cache, n_head_kv, params, batch, out, workspace,
+                                 err_flag)
+    _lib.check("iian_pa_write_attention", _lib.load().iian_pa_write_attention(*args))
+    return out
+
+
+def bind_write_paged_attn(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, k_cache: KVPool,
+                          v_cache: KVPool, n_head_kv: int, params: PagedAttnParams, batch: PagedBatch,
+                          out: torch.Tensor, workspace: torch.Tensor,
+                          err_flag: Optional[torch.Tensor] = None) -> Callable[[], None]:
+    """write_paged_attn checked once and bound to these buffers and the
+    current stream, as bind_paged_attn."""
+    _, args = _write_attn_args(q, k_new, v_new, k_cache, v_cache, n_head_kv, params, batch, out, workspace,
+                               err_flag)
+    fn = _lib.load().iian_pa_write_attention
+
+    def call() -> None:
+        st = fn(*args)
+        if st:
+            _lib.check("iian_pa_write_attention", st)
+    return call
+
+
 def dequant_q8_0(pool: KVPool, rows_idx: torch.Tensor) -> torch.Tensor:
     """f32 values of the given Q8_0 pool rows (ggml-quants.c:553-567)."""
     if pool.type != GGML_TYPE_Q8_0:

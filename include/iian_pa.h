@@ -174,6 +174,37 @@ int iian_pa_attention_noalloc(void *stream, const float *q, const void *k_pool, 
                               float scale, float softcap, int32_t causal, int32_t n_swa,
                               float *out, int32_t *err_flag);
 
+/* The layer's KV write and its attention call in one launch, for decode
+ * steps: replaces the set_rows of the step's new K and V rows
+ * (src/iian/graph.cpp:319-320, iian_pa_kv_write_kv here) followed by the
+ * paged attention op (src/iian/graph.cpp:331-336, paged_attn.cpp:90-169,
+ * iian_pa_attention here).  New token t's rows k_new[t], v_new[t] (f32
+ * [T][n_head_kv*head_dim], 16-byte aligned) are stored, converted to f16 as
+ * iian_pa_kv_write converts them, at the cell of its position:
+ * block_tables[s][pos[t] / block_size] * block_size + pos[t] % block_size for
+ * its sequence s (the slot iian_pa_build_batch computes); then every query
+ * attends as iian_pa_attention would after that write.  Pools, outputs and
+ * err_flag bits 1 and 2 equal those of the two calls, bit for bit.  Bit 0: a
+ * new token whose position is outside [0, seq_lens[s]) or whose block id is
+ * outside [0, num_blocks) is not written (the two calls write a slot inside
+ * the pool in the second case).  Supported where the call runs the f16
+ * decode kernels: f16 pools with head_dim == head_dim_v in {64, 96, 128, 256},
+ * a power-of-two block_size of at least 8, max_query_len * n_head / n_head_kv
+ * <= 32 (decode and spec-verify steps); anything else returns
+ * IIAN_PA_ERR_UNSUPPORTED before any launch, and the caller makes the two
+ * calls instead.  Within one call, two new tokens of one sequence at the same
+ * position race, as two equal slots of one iian_pa_kv_write call do. */
+int iian_pa_write_attention(void *stream, const float *q, const float *k_new, const float *v_new,
+                            void *k_pool, void *v_pool, int type_k, int type_v, int32_t num_blocks,
+                            const int32_t *block_tables, int32_t max_blocks,
+                            const int32_t *seq_lens, const int32_t *query_start_loc,
+                            const int32_t *pos, int32_t n_tokens, int32_t n_seqs,
+                            int32_t max_query_len, int32_t n_head, int32_t n_head_kv,
+                            int32_t head_dim, int32_t head_dim_v, int32_t block_size,
+                            float scale, float softcap, int32_t causal, int32_t n_swa,
+                            float *out, void *workspace, size_t workspace_bytes,
+                            int32_t *err_flag);
+
 /* Builds the arrays iian_pa_attention and iian_pa_kv_write read for one
  * engine step on the device, from the per-request state the scheduler holds,
  * in place of the host loop of Engine::step that expands every request's

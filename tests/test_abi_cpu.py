@@ -110,6 +110,39 @@ def test_attention_rejects_invalid_arguments(lib, over, code):
     assert call_attention(lib, **over) == code
 
 
+def call_write_attention(lib, **over):
+    """iian_pa_write_attention with fake aligned addresses, as call_attention."""
+    a = dict(stream=None, q=0x1000, kn=0x10000, vn=0x11000, k=0x2000, v=0x3000, tk=1, tv=1, num_blocks=64,
+             bt=0x4000, max_blocks=4, seq_lens=0x5000, qsl=0x6000, pos=0x7000, T=4, S=2, maxq=2, H=8, Hkv=2, D=128,
+             Dv=128, bs=16, scale=0.1, softcap=0.0, causal=1, n_swa=0, out=0x8000, ws=0x9000, ws_bytes=1 << 30,
+             err=None)
+    a.update(over)
+    return lib.iian_pa_write_attention(a["stream"], a["q"], a["kn"], a["vn"], a["k"], a["v"], a["tk"], a["tv"],
+                                       a["num_blocks"], a["bt"], a["max_blocks"], a["seq_lens"], a["qsl"], a["pos"],
+                                       a["T"], a["S"], a["maxq"], a["H"], a["Hkv"], a["D"], a["Dv"], a["bs"],
+                                       a["scale"], a["softcap"], a["causal"], a["n_swa"], a["out"], a["ws"],
+                                       a["ws_bytes"], a["err"])
+
+
+@pytest.mark.parametrize("over,code", [
+    ({"kn": None}, -1), ({"vn": None}, -1), ({"q": None}, -1), ({"kn": 0x10004}, -2), ({"vn": 0x11008}, -2),
+    ({"tk": 8, "tv": 8}, -3),                        # Q8_0 pools: the two calls
+    ({"tk": 0, "tv": 0}, -3),                        # f32 pools (the general kernel)
+    ({"D": 128, "Dv": 64}, -3),                      # K and V head sizes differ
+    ({"D": 80, "Dv": 80}, -3),                       # a head size only the general kernel takes
+    ({"bs": 4}, -3),                                 # blocks below 8 cells
+    ({"T": 40, "maxq": 20}, -3),                     # 80 rows per kv head: a prefill call
+    ({"ws": None}, -4),
+])
+def test_write_attention_rejects_calls_outside_the_decode_kernels(lib, over, code):
+    assert call_write_attention(lib, **over) == code
+
+
+def test_write_attention_empty_batch_is_ok(lib):
+    assert call_write_attention(lib, T=0) == 0
+    assert call_write_attention(lib, S=0, kn=None) == 0
+
+
 def test_attention_empty_batch_is_ok(lib):
     assert call_attention(lib, T=0) == 0
     assert call_attention(lib, S=0) == 0
