@@ -170,3 +170,39 @@ def test_write_attention_refuses_other_calls_before_any_launch(pa):
     torch.cuda.synchronize()
     assert torch.equal(kp.data, before[0]) and torch.equal(vp.data, before[1])
     assert torch.equal(w.k_pool.data, before_q8)
+
+
+@pytest.mark.parametrize("name", ["sk_d128_spec2", "seg_d128_spec2"])
+def test_write_attention_graph_replays(pa, name):
+    """The fused call captured in a graph (it allocates nothing) and replayed
+    four times, with the pools reset to their contents before the write and
+    an eager call of other new rows in between: every replay gives the eager
+    fused call's pools and output, bit for bit."""
+    c, k, v, batch, k_new, v_new, prm = case_inputs(pa, name)
+    banner(f"write+attention graph replays {name}")
+    q = torch.as_tensor(c.q).cuda()
+    k0, v0 = k.data.clone(), v.data.clone()
+    ws = pa.new_workspace(c.T, batch.n_seqs, c.H, c.Hkv, c.D, c.bt.shape[1], c.bs)
+    out = torch.empty((c.T, c.H, c.D), dtype=torch.float32, device="cuda")
+    want = pa.write_paged_attn(q, k_new, v_new, k, v, c.Hkv, prm, batch, workspace=ws).clone()
+    want_k, want_v = k.data.clone(), v.data.clone()
+    k_other, v_other = torch.randn_like(k_new), torch.randn_like(v_new)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):   # warm-up outside the capture
+        pa.write_paged_attn(q, k_new, v_new, k, v, c.Hkv, prm, batch, out=out, workspace=ws)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        pa.write_paged_attn(q, k_new, v_new, k, v, c.Hkv, prm, batch, out=out, workspace=ws)
+    for it in range(4):
+        k.data.copy_(k0)
+        v.data.copy_(v0)
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int32), want.view(torch.int32)), it
+        assert torch.equal(k.data, want_k) and torch.equal(v.data, want_v), it
+        pa.write_paged_attn(q, k_other, v_other, k, v, c.Hkv, prm, batch, workspace=ws)   # eager, other rows
+        torch.cuda.synchronize()
